@@ -1,0 +1,220 @@
+/* svla.h — C-ABI of the MI355X (gfx950) SmolVLA bf16 hot-path library.
+ *
+ * Drop-in boundary for the reference's per-kernel AIE ABI
+ * (`extern "C" void f(T in[R][C], ..., T out[R][C])`, caller-owned buffers,
+ * outputs written in place, e.g. cc/bf16/rms_norm_960_bf16.cc:60) and for the
+ * host tiling helpers that drive it from numpy (vla/text_encoder_bf16.py:398-475,
+ * vla/action_expert_bf16.py:517-655).  Unlike the AIE ABI the shapes are
+ * runtime arguments and every entry point reports errors.
+ *
+ * Conventions
+ *  - All pointers are DEVICE pointers (hipMalloc / torch CUDA tensors) unless
+ *    the parameter is documented as a host value.  bf16 tensors are IEEE
+ *    bfloat16 (2 bytes), row-major with explicit leading dimensions counted in
+ *    elements.  16-byte alignment and leading dimensions that are multiples of
+ *    8 elements are required where noted ("aligned").
+ *  - Linear weights are consumed PACKED as [N, K] (out-features x in-features,
+ *    K contiguous, i.e. nn.Linear's own layout).  The reference stores them
+ *    [in, out] (vla/text_encoder_bf16.py:601-611); svla_pack_weight_bf16 turns
+ *    one into the other on the device.
+ *  - Caller owns all memory, including workspaces; the library allocates
+ *    nothing per call and keeps no per-call state.  Calls are asynchronous on
+ *    the given stream (NULL = default stream) and may be captured in a HIP
+ *    graph (no memset / allocation inside).
+ *  - Return value: 0 on success, SVLA_EINVAL for bad shapes/alignment, or a
+ *    hipError_t (positive) from the launch.
+ */
+#ifndef SVLA_H
+#define SVLA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SVLA_OK 0
+#define SVLA_EINVAL (-22)
+
+typedef void* svla_stream_t; /* hipStream_t */
+
+/* activation codes (svla_linear_bf16 `act`) */
+#define SVLA_ACT_NONE 0
+#define SVLA_ACT_GELU_TANH 1
+#define SVLA_ACT_GELU_ERF 2
+#define SVLA_ACT_SILU 3
+
+/* attention mask kinds */
+#define SVLA_MASK_NONE 0
+#define SVLA_MASK_CAUSAL 1
+#define SVLA_MASK_PREFIX_LM 2
+
+/* Library version (major*10000 + minor*100 + patch). */
+int svla_version(void);
+
+/* ---------------------------------------------------------------- norms --
+ * RMSNorm, y = x * rsqrt(mean(x^2) + eps) * w, fp32 math, one bf16 rounding.
+ * Replaces rms_norm_960_bf16(bf16[4][960], bf16[960], bf16[4][960])
+ * (cc/bf16/rms_norm_960_bf16.cc:60), rms_norm_bf16 (cc/bf16_old/rms_norm_bf16.cc:60)
+ * and the tiling helper rmsnorm() (vla/text_encoder_bf16.py:398-404).
+ * cols % 8 == 0, cols <= 2048, aligned. */
+int svla_rmsnorm_bf16(const void* x, int ldx, const void* w, void* y, int ldy, int rows,
+                      int cols, float eps, svla_stream_t stream);
+
+/* LayerNorm with affine gamma/beta (beta may be NULL).
+ * Replaces layer_norm_bf16 + the bias kernel (cc/bf16_old/layer_norm_bf16.cc:67;
+ * vla/vision_block_bf16.py:101-127) and layernorm() (:272-280). */
+int svla_layernorm_bf16(const void* x, int ldx, const void* gamma, const void* beta, void* y,
+                        int ldy, int rows, int cols, float eps, svla_stream_t stream);
+
+/* ----------------------------------------------------------------- GEMM --
+ * C[M,N] = epilogue(alpha * A[M,K] . W[N,K]^T) on bf16 MFMA (fp32 accumulate).
+ * Replaces the Allo GEMM module GEMM(M,N,K,Pm,Pn,Pk,bf16,bf16) and its K-chunk
+ * host accumulation (vla/text_encoder_bf16.py:174-225, 584-590; contract
+ * cc/gemm.py:44-77), the attention-score kernel transpose_matmul_with_scale_bf16
+ * (cc/bf16_old/transpose_matmul_with_scale_bf16.cc:52, alpha = 0.125) and the
+ * residual adds (vla/text_encoder_bf16.py:532,592).
+ * Epilogue order (mirrors the torch modules' bf16 boundaries):
+ *   v = alpha*acc (+ bias[n]) (+ bias_f32[n]); if out_f32: store fp32 v.
+ *   else v = bf16(v); v = bf16(act(v)); if res: v = bf16(v + res[m,n]); store.
+ * bias/bias_f32/res may be NULL.  K % 8 == 0, N % 4 == 0, aligned.
+ * `ws` is an fp32 workspace for split-K (may be NULL: no split), `ws_bytes`
+ * its size; the library picks a split count that fits. */
+int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
+                     const float* bias_f32, const void* res, int ldr, void* c, int ldc, int m,
+                     int n, int k, float alpha, int act, int out_f32, float* ws, long ws_bytes,
+                     svla_stream_t stream);
+
+/* Fused QKV projection with rotate-half RoPE in the epilogue.
+ * Columns [0, rope_cols) are heads of 64 that get RoPE at position
+ * (row % seq_len) with fp32 tables cos/sin [seq_len, 32]; the remaining columns
+ * (V) are stored as projected.  Replaces gemm_q/gemm_kv + rope_apply_packed
+ * (vla/text_encoder_bf16.py:422-475, 491-500; kernels cc/float/rope_vec_ops.cc,
+ * sine.cc, cosine.cc).  rope_cols % 64 == 0. */
+int svla_linear_rope_bf16(const void* a, int lda, const void* w, int ldw, void* c, int ldc,
+                          int m, int n, int k, int rope_cols, int seq_len, const float* cos_t,
+                          const float* sin_t, float* ws, long ws_bytes, svla_stream_t stream);
+
+/* Gated MLP up-projection: out[M, inter] = bf16(silu(gate) ) * bf16(up), gate/up
+ * from one GEMM over the interleaved weight produced by svla_pack_gate_up_bf16.
+ * Replaces gemm_ffn_up x2 + silu_*_bf16 + the numpy hadamard
+ * (vla/text_encoder_bf16.py:537-581; vla/action_expert_bf16.py:629-642). */
+int svla_linear_silu_mul_bf16(const void* a, int lda, const void* w_gu, int ldw, void* out,
+                              int ldo, int m, int inter, int k, float* ws, long ws_bytes,
+                              svla_stream_t stream);
+
+/* Patch embedding: Conv2d(C -> E, kernel = stride = P) as an im2col GEMM over
+ * images [n_img, C, H, H] bf16, + conv bias, + learned position embedding
+ * pos[(H/P)^2, E].  out [n_img*(H/P)^2, E].  w is the conv weight [E, C*P*P].
+ * Replaces preprocessing_block/conv2d (vla/preprocessing_bf16.py:86-109;
+ * cc/bf16_old/conv_bf16.cc:12) + the position add (vla/vit_emb.py:43-47). */
+int svla_patch_embed_bf16(const void* images, const void* w, const void* bias, const void* pos,
+                          void* out, int ldo, int n_img, int chans, int image, int patch,
+                          int embed, float* ws, long ws_bytes, svla_stream_t stream);
+
+/* Pixel-shuffle connector: out = pixel_shuffle(x, scale) . W^T with the shuffle
+ * folded into the A-operand addressing.  x [n_img, grid*grid, hidden];
+ * out rows are n_img*(grid/scale)^2, ldo.  Replaces connector_block/fused_op
+ * (vla/connector_bf16.py:97-139; formula vla/vla.py:434-437). */
+int svla_connector_bf16(const void* x, const void* w, int ldw, void* out, int ldo, int n_img,
+                        int grid, int hidden, int scale, int n_out, float* ws, long ws_bytes,
+                        svla_stream_t stream);
+
+/* Action output projection fused with the Euler update of the flow-matching
+ * loop: v = bf16(A . W^T); x_f32 += dt * v; x_bf16 = bf16(x_f32) (x_bf16 may be
+ * NULL).  Replaces postprocessing's GEMM (vla/vla.py:218-222) and adds the
+ * update the reference lacks. */
+int svla_action_out_euler(const void* a, int lda, const void* w, int ldw, float* x_f32,
+                          int ldx, void* x_bf16, int ldxb, int m, int n, int k, float dt,
+                          svla_stream_t stream);
+
+/* ------------------------------------------------------------ attention --
+ * Fused GQA attention: O = softmax(scale * Q K^T + mask) V per head, query
+ * head h reading KV head h*hkv/hq.  Scores and softmax statistics fp32,
+ * probabilities bf16 into the P.V MFMA, fp32 accumulate, bf16 out.
+ * Q row r of batch b at q + b*q_bs + r*ldq + h*64 (same scheme for k, v, o).
+ * head_dim must be 64.  mask: SVLA_MASK_NONE / CAUSAL / PREFIX_LM (keys
+ * < prefix_len visible to all rows, later keys causal).
+ * Replaces the per-head score GEMMs, masked_softmax_128_bf16 / softmax_bf16_* /
+ * softmax_float32_seq1024 and the P.V GEMMs (vla/text_encoder_bf16.py:502-526;
+ * vla/vision_block_bf16.py:325-367; vla/action_expert_bf16.py:689-713, 764-787). */
+int svla_attention_bf16(const void* q, int ldq, long q_bs, const void* k, int ldk, long k_bs,
+                        const void* v, int ldv, long v_bs, void* o, int ldo, long o_bs,
+                        int batch, int sq, int sk, int hq, int hkv, int head_dim, float scale,
+                        int mask_kind, int prefix_len, svla_stream_t stream);
+
+/* -------------------------------------------------- per-kernel harness --
+ * Standalone kernels matching the reference's per-kernel test harness. */
+
+/* masked_softmax_128_bf16(bf16[R][C], int row_start, bf16[R][C])
+ * (cc/bf16/masked_softmax_128_bf16.cc:251): causal mask at global row
+ * row_start + r, fp32 softmax, bf16 out.  row_start is a HOST int. */
+int svla_masked_softmax_bf16(const void* s, int row_start, void* p, int rows, int cols,
+                             svla_stream_t stream);
+
+/* Row softmax, input bf16 (in_f32 = 0) or fp32 (in_f32 = 1), output bf16
+ * (out_f32 = 0) or fp32.  softmax_bf16_* (cc/bf16_old/v2_softmax_bf16.cc:552-663,
+ * v1_softmax_bf16.cc:159) and softmax_float32_seq1024 (cc/float/v1_softmax_float.cc:117). */
+int svla_softmax(const void* s, void* p, int rows, int cols, int in_f32, int out_f32,
+                 svla_stream_t stream);
+
+/* SiLU y = x * sigmoid(x) on n bf16 values (silu_{128,160,256}_bf16,
+ * cc/bf16/silu_160_bf16.cc:124; silu_bf16 cc/bf16_old/silu_bf16.cc:192). */
+int svla_silu_bf16(const void* x, void* y, long n, svla_stream_t stream);
+
+/* GELU (kind = SVLA_ACT_GELU_TANH or SVLA_ACT_GELU_ERF) on n bf16 values
+ * (gelu_bf16, cc/bf16_old/gelu_bf16.cc:83). */
+int svla_gelu_bf16(const void* x, void* y, long n, int kind, svla_stream_t stream);
+
+/* out = bf16(silu(gate)) * up (bf16), n values (the numpy hadamard step,
+ * vla/text_encoder_bf16.py:581). */
+int svla_silu_mul_bf16(const void* gate, const void* up, void* out, long n,
+                       svla_stream_t stream);
+
+/* RoPE on x [rows, heads*64] (leading dim ldx) at positions pos_offset+row,
+ * fp32 tables [>= pos_offset+rows, 32].  in_f32/out_f32 select fp32 or bf16
+ * storage.  rope_fused_float32 (cc/float/rope_fused.cc:17) and
+ * rope_apply_packed (vla/text_encoder_bf16.py:422-475). */
+int svla_rope(const void* x, int ldx, void* y, int ldy, int rows, int heads,
+              const float* cos_t, const float* sin_t, int pos_offset, int in_f32, int out_f32,
+              svla_stream_t stream);
+
+/* ---------------------------------------------------------- utilities -- */
+
+/* RoPE tables: cos/sin[pos][k] of pos / theta^(2k/head_dim), fp32,
+ * pos < max_pos, k < head_dim/2 (apply_rope, vla/text_encoder_bf16.py:80-97). */
+int svla_rope_table(float* cos_t, float* sin_t, int max_pos, int head_dim, float theta,
+                    svla_stream_t stream);
+
+/* Transpose-pack a reference [K, N] (in x out) bf16 weight to [N, K]. */
+int svla_pack_weight_bf16(const void* w_kn, int ldw, void* out_nk, int k, int n,
+                          svla_stream_t stream);
+
+/* Interleave gate/up weights ([K, inter] each, reference layout) into the
+ * [2*inter, K] layout consumed by svla_linear_silu_mul_bf16 (blocks of 16 rows
+ * alternating gate/up).  inter % 16 == 0. */
+int svla_pack_gate_up_bf16(const void* w_gate, const void* w_up, void* out, int k, int inter,
+                           svla_stream_t stream);
+
+/* Language embedding: out[r] = bf16(table[ids[r]] * scale) for r < n_tokens;
+ * ids are int64 (an id outside [0, vocab) yields a zero row).  Row r goes to
+ * out + (r / per_sample)*out_bs + (r % per_sample)*ldo
+ * (create_text_emb, vla/vla.py:169-174). */
+int svla_embed_bf16(const int64_t* ids, const void* table, long vocab, int hidden, float scale,
+                    void* out, int ldo, long out_bs, long n_tokens, int per_sample,
+                    svla_stream_t stream);
+
+/* Sinusoidal flow-matching time embedding of the HOST scalar t, computed in
+ * fp64 and rounded to bf16: [sin(2 pi t / p_j) | cos(2 pi t / p_j)], p_j
+ * geometric from min_period to max_period, out [dim] bf16. */
+int svla_time_embedding_bf16(double t, int dim, double min_period, double max_period, void* out,
+                             svla_stream_t stream);
+
+/* fp32 -> bf16 conversion (round to nearest even), n values. */
+int svla_f32_to_bf16(const float* x, void* y, long n, svla_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SVLA_H */

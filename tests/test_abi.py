@@ -1,0 +1,48 @@
+"""CPU-side checks of the drop-in boundary: ``libsvla.so`` loads, exports every
+entry point declared in ``include/svla.h``, and the ctypes table covers them
+all (no compute calls: there is no GPU here)."""
+
+import ctypes
+import pathlib
+import re
+
+import pytest
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "svla.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\bint\s+(svla_\w+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    assert "svla_linear_bf16" in syms and "svla_attention_bf16" in syms
+    assert len(syms) >= 20
+
+
+def test_library_exports_every_declared_symbol():
+    from smolvla import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libsvla.so is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, f"declared but not exported: {missing}"
+
+
+def test_ctypes_table_matches_header():
+    from smolvla import _lib
+    assert sorted(_lib.SIGNATURES) == declared_symbols()
+    lib = _lib.load()
+    assert lib.svla_version() == 100
+
+
+def test_ops_refuse_cpu_tensors():
+    import torch
+    from smolvla import ops
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        ops.rmsnorm(x, torch.ones(64, dtype=torch.bfloat16), 1e-5)

@@ -1,0 +1,328 @@
+"""Kernel-level parity: each HIP kernel (through the C-ABI) vs the CPU oracle
+(``oracle/smolvla_ref.py``) or the torch fp32 formula it mirrors, on seeded
+inputs.  Tolerances (written per test):
+
+* bf16 GEMM / fused-epilogue outputs: max |got - want| / max |want| <= 1e-2
+  (the per-layer-output bound) and elementwise allclose at the reference
+  harness tolerance (atol 1e-1, rtol 1e-2, gemm/v1_test_tiled_gemm.py:150-151);
+* norms / elementwise: <= 1 bf16 ulp relative (2^-7) plus atol 1e-2;
+* attention: max relative error <= 1e-2.
+"""
+
+import math
+
+import pytest
+import torch
+
+import oracle.smolvla_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from smolvla import ops as _ops
+    from smolvla import _lib
+    _lib.load()
+    return _ops
+
+
+def rel_err(got, want):
+    got, want = got.float().cpu(), want.float().cpu()
+    return ((got - want).abs().max() / want.abs().max().clamp_min(1e-6)).item()
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def randn(g, *shape, std=1.0):
+    return (torch.randn(*shape, generator=g) * std).to(BF16)
+
+
+def assert_close_bf16(got, want, rel=1e-2, atol=1e-1, rtol=1e-2):
+    got_c, want_c = got.float().cpu(), want.float().cpu()
+    assert torch.isfinite(got_c).all()
+    e = rel_err(got_c, want_c)
+    assert e <= rel, f"max relative error {e:.3e} > {rel}"
+    torch.testing.assert_close(got_c, want_c, atol=atol, rtol=rtol)
+
+
+# ------------------------------------------------------------------ norms ---
+@pytest.mark.parametrize("rows,cols,eps", [(4, 960, 1e-6), (241, 960, 1e-5), (50, 720, 1e-5),
+                                           (3, 2048, None), (1, 64, 1e-5)])
+def test_rmsnorm(ops, rows, cols, eps):
+    g = gen(1)
+    x = randn(g, rows, cols)
+    w = (1 + 0.1 * torch.randn(cols, generator=g)).to(BF16)
+    got = ops.rmsnorm(x.cuda(), w.cuda(), eps)
+    want = ref.rms_norm(x, w, eps)
+    torch.testing.assert_close(got.cpu().float(), want.float(), atol=1e-2, rtol=2 ** -7)
+
+
+def test_rmsnorm_strided_rows(ops):
+    g = gen(2)
+    big = randn(g, 10, 1024)
+    x = big[:, :960]                               # leading dim 1024
+    w = randn(g, 960)
+    out = torch.zeros(10, 1024, dtype=BF16, device="cuda")
+    ops.rmsnorm(big.cuda()[:, :960], w.cuda(), 1e-5, out=out[:, :960])
+    torch.testing.assert_close(out[:, :960].cpu().float(), ref.rms_norm(x, w, 1e-5).float(),
+                               atol=1e-2, rtol=2 ** -7)
+    assert (out[:, 960:] == 0).all()
+
+
+@pytest.mark.parametrize("rows,cols", [(1024, 768), (4, 768), (7, 128)])
+def test_layernorm(ops, rows, cols):
+    g = gen(3)
+    x = (torch.randn(rows, cols, generator=g) * 2 + 0.5).to(BF16)
+    gm = (1 + 0.1 * torch.randn(cols, generator=g)).to(BF16)
+    bt = randn(g, cols, std=0.1)
+    got = ops.layernorm(x.cuda(), gm.cuda(), bt.cuda(), 1e-6)
+    want = ref.layer_norm(x, gm, bt, 1e-6)
+    torch.testing.assert_close(got.cpu().float(), want.float(), atol=1e-2, rtol=2 ** -7)
+
+
+# ------------------------------------------------------------------- GEMM ---
+GEMM_SHAPES = [
+    (1, 32, 32), (50, 960, 720), (50, 720, 960), (50, 32, 720), (128, 960, 960),
+    (241, 1600, 960), (241, 960, 2560), (192, 960, 12288), (1024, 2304, 768),
+    (1024, 768, 3072), (3, 720, 1440), (77, 100, 24),
+]
+
+
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+@pytest.mark.parametrize("split", [True, False])
+def test_linear(ops, M, N, K, split):
+    g = gen(M * 7 + N + K)
+    a = randn(g, M, K)
+    w = randn(g, K, N, std=0.02)
+    wp = ops.pack_weight(w.cuda())
+    torch.testing.assert_close(wp.cpu(), w.t().contiguous())
+    got = ops.linear(a.cuda(), wp, ws=None if split else False)
+    want = ref.linear(a, w)
+    assert_close_bf16(got, want)
+
+
+def test_linear_bias_act_residual(ops):
+    g = gen(11)
+    M, N, K = 130, 3072, 768
+    a, w, b = randn(g, M, K), randn(g, K, N, std=0.02), randn(g, N, std=0.02)
+    wp = ops.pack_weight(w.cuda())
+    got = ops.linear(a.cuda(), wp, bias=b.cuda(), act="gelu_tanh")
+    want = ref.gelu(ref.linear(a, w, b), "tanh")
+    assert_close_bf16(got, want)
+    res = randn(g, M, N)
+    got = ops.linear(a.cuda(), wp, bias=b.cuda(), res=res.cuda())
+    want = ref.linear(a, w, b) + res
+    assert_close_bf16(got, want)
+    got = ops.linear(a.cuda(), wp, act="silu", ws=False)
+    assert_close_bf16(got, ref.silu(ref.linear(a, w)))
+    bf = torch.randn(N, generator=g) * 0.1
+    got = ops.linear(a.cuda(), wp, bias_f32=bf.cuda(), out_f32=True)
+    want = a.float() @ w.float() + bf
+    assert rel_err(got, want) < 1e-3
+
+
+def test_linear_alpha_attn_score_harness(ops):
+    # transpose_matmul_with_scale_bf16: C = 0.125 * A . B^T
+    # (attn_score/test_attn_score_bf16.py:62-66)
+    from smolvla import kernels
+    g = gen(12)
+    for (M, N) in ((64, 64), (128, 128)):
+        A, B = randn(g, M, 64), randn(g, N, 64)
+        C = torch.empty(M, N, dtype=BF16, device="cuda")
+        kernels.transpose_matmul_with_scale_bf16(A.cuda(), B.cuda(), C)
+        want = (A.float() @ B.float().t() * 0.125).to(BF16)
+        torch.testing.assert_close(C.cpu().float(), want.float(), atol=1e-1, rtol=1e-2)
+
+
+@pytest.mark.parametrize("M,L,hid,split", [(128, 128, 960, True), (241, 241, 960, False),
+                                           (482, 241, 960, True), (50, 50, 720, True),
+                                           (100, 50, 720, False)])
+def test_linear_rope_qkv(ops, M, L, hid, split):
+    g = gen(M + hid)
+    theta = 100000.0
+    x = randn(g, M, hid)
+    wq, wk, wv = randn(g, hid, 960, std=0.02), randn(g, hid, 320, std=0.02), randn(g, hid, 320,
+                                                                                   std=0.02)
+    w = torch.cat([wq, wk, wv], dim=1)
+    cos_t, sin_t = ops.rope_table(L, 64, theta)
+    c_ref, s_ref = ref.rope_tables(L, 64, theta)
+    # angles reach ~240 rad: a 1-2 ulp fp32 difference in the angle (powf) is ~4e-6
+    torch.testing.assert_close(cos_t.cpu(), c_ref, atol=1e-5, rtol=0)
+    torch.testing.assert_close(sin_t.cpu(), s_ref, atol=1e-5, rtol=0)
+    got = ops.linear_rope(x.cuda(), ops.pack_weight(w.cuda()), 1280, L, cos_t, sin_t,
+                          ws=None if split else False).cpu()
+    B = M // L
+    q = ref.apply_rope(ref.linear(x, wq).view(B, L, 15, 64), theta).to(BF16).view(M, 960)
+    k = ref.apply_rope(ref.linear(x, wk).view(B, L, 5, 64), theta).to(BF16).view(M, 320)
+    v = ref.linear(x, wv)
+    assert_close_bf16(got[:, :960], q)
+    assert_close_bf16(got[:, 960:1280], k)
+    assert_close_bf16(got[:, 1280:], v)
+
+
+@pytest.mark.parametrize("M,K,inter,split", [(50, 720, 2048, True), (241, 960, 2560, False),
+                                             (1024, 960, 2560, True), (5, 64, 48, False)])
+def test_linear_silu_mul(ops, M, K, inter, split):
+    g = gen(M + K)
+    x = randn(g, M, K)
+    wg, wu = randn(g, K, inter, std=0.02), randn(g, K, inter, std=0.02)
+    wgu = ops.pack_gate_up(wg.cuda(), wu.cuda())
+    got = ops.linear_silu_mul(x.cuda(), wgu, ws=None if split else False)
+    want = ref.silu(ref.linear(x, wg)) * ref.linear(x, wu)
+    assert_close_bf16(got, want)
+
+
+def test_patch_embed(ops):
+    g = gen(21)
+    n, C, H, P, E = 3, 3, 512, 16, 768
+    img = (torch.rand(n, C, H, H, generator=g) * 2 - 1).to(BF16)
+    kern = randn(g, E, C, P, P, std=0.02)
+    bias = randn(g, E, std=0.02)
+    pos = randn(g, (H // P) ** 2, E, std=0.02)
+    got = ops.patch_embed(img.cuda(), kern.reshape(E, -1).cuda(), bias.cuda(), pos.cuda(), P)
+    want = ref.patch_embed(img, kern, bias, pos).reshape(-1, E)
+    assert_close_bf16(got, want)
+
+
+def test_connector(ops):
+    g = gen(22)
+    x = randn(g, 3, 1024, 768)
+    w = randn(g, 12288, 960, std=0.02)
+    got = ops.connector(x.cuda(), ops.pack_weight(w.cuda()), 4)
+    want = ref.connector(x, w, 4).reshape(-1, 960)
+    assert_close_bf16(got, want)
+
+
+def test_action_out_euler(ops):
+    g = gen(23)
+    M, N, K = 100, 32, 720
+    a, w = randn(g, M, K), randn(g, K, N, std=0.02)
+    x = torch.randn(M, N, generator=g)
+    xd = x.cuda().clone()
+    xb = torch.empty(M, N, dtype=BF16, device="cuda")
+    ops.action_out_euler(a.cuda(), ops.pack_weight(w.cuda()), xd, -0.1, x_bf16=xb)
+    v = ref.linear(a, w).float()
+    want = x + (-0.1) * v
+    assert rel_err(xd, want) < 1e-3
+    torch.testing.assert_close(xb.cpu(), xd.cpu().to(BF16))
+
+
+# -------------------------------------------------------------- attention ---
+ATTN_CASES = [
+    # B, Sq, Sk, hq, hkv, mask, prefix
+    (1, 128, 128, 15, 5, "causal", 0),
+    (1, 241, 241, 15, 5, "prefix_lm", 240),
+    (2, 241, 241, 15, 5, "prefix_lm", 240),
+    (1, 50, 50, 15, 5, "causal", 0),
+    (3, 50, 241, 15, 5, "none", 0),
+    (1, 1024, 1024, 12, 12, "none", 0),
+    (2, 17, 17, 3, 1, "prefix_lm", 16),
+    (1, 1, 5, 2, 1, "none", 0),
+]
+
+
+@pytest.mark.parametrize("B,Sq,Sk,hq,hkv,mask,prefix", ATTN_CASES)
+def test_attention(ops, B, Sq, Sk, hq, hkv, mask, prefix):
+    g = gen(B * 1000 + Sq + hq)
+    q = randn(g, B, Sq, hq * 64)
+    k = randn(g, B, Sk, hkv * 64)
+    v = randn(g, B, Sk, hkv * 64)
+    out = torch.empty(B, Sq, hq * 64, dtype=BF16, device="cuda")
+    ops.attention(q.cuda(), k.cuda(), v.cuda(), out, hq, hkv, mask=mask, prefix_len=prefix)
+    m = ref.make_mask(mask, Sq, Sk, prefix)
+    want = ref.gqa_attention(q.view(B, Sq, hq, 64).float(), k.view(B, Sk, hkv, 64),
+                             v.view(B, Sk, hkv, 64), m)
+    assert rel_err(out, want) <= 1e-2
+    torch.testing.assert_close(out.cpu().float(), want.float(), atol=2e-2, rtol=2e-2)
+
+
+def test_attention_views_into_fused_qkv(ops):
+    # Q/K/V as column slices of one [B*S, 1600] projection buffer
+    g = gen(31)
+    B, S = 2, 241
+    qkv = randn(g, B, S, 1600)
+    d = qkv.cuda()
+    out = torch.empty(B, S, 960, dtype=BF16, device="cuda")
+    ops.attention(d[:, :, :960], d[:, :, 960:1280], d[:, :, 1280:], out, 15, 5, "causal")
+    want = ref.gqa_attention(qkv[:, :, :960].reshape(B, S, 15, 64).float(),
+                             qkv[:, :, 960:1280].reshape(B, S, 5, 64),
+                             qkv[:, :, 1280:].reshape(B, S, 5, 64), ref.make_mask("causal", S, S))
+    assert rel_err(out, want) <= 1e-2
+
+
+# ------------------------------------------------------------ elementwise ---
+def test_silu_gelu_silu_mul(ops):
+    g = gen(41)
+    x = randn(g, 4, 2560, std=3.0)
+    torch.testing.assert_close(ops.silu(x.cuda()).cpu(), ref.silu(x), atol=1e-2, rtol=2 ** -7)
+    torch.testing.assert_close(ops.gelu(x.cuda(), "tanh").cpu(), ref.gelu(x, "tanh"),
+                               atol=1e-2, rtol=2 ** -7)
+    torch.testing.assert_close(ops.gelu(x.cuda(), "erf").cpu(), ref.gelu(x, "erf"),
+                               atol=1e-2, rtol=2 ** -7)
+    u = randn(g, 4, 2560)
+    torch.testing.assert_close(ops.silu_mul(x.cuda(), u.cuda()).cpu(), ref.silu(x) * u,
+                               atol=1e-2, rtol=2 ** -7)
+    odd = randn(g, 13)                                   # non-multiple-of-8 tail
+    torch.testing.assert_close(ops.silu(odd.cuda()).cpu(), ref.silu(odd), atol=1e-2,
+                               rtol=2 ** -7)
+
+
+def test_softmax_kernels(ops):
+    g = gen(42)
+    s = randn(g, 8, 128, std=2.0)
+    for rs in (0, 96):
+        got = ops.masked_softmax(s.cuda(), rs).cpu()
+        torch.testing.assert_close(got.float(), ref.masked_softmax_rows(s, rs).float(),
+                                   atol=5e-3, rtol=5e-2)
+    s32 = torch.randn(24, 1024, generator=g) * 3
+    got = ops.softmax(s32.cuda(), out_f32=True).cpu()
+    torch.testing.assert_close(got, torch.softmax(s32, -1), atol=1e-6, rtol=1e-4)
+    got = ops.softmax(s.cuda()).cpu()
+    torch.testing.assert_close(got.float(), ref.softmax_rows(s).float(), atol=5e-3, rtol=2e-2)
+
+
+def test_rope_standalone(ops):
+    g = gen(43)
+    L, H = 64, 8
+    x = torch.randn(L, H * 64, generator=g)
+    c, s = ops.rope_table(L, 64, 10000.0)
+    got = ops.rope(x.cuda(), H, c, s).cpu()
+    want = ref.apply_rope(x.view(1, L, H, 64), 10000.0).view(L, H * 64)
+    torch.testing.assert_close(got, want, rtol=1e-3, atol=1e-4)
+
+
+def test_embed_and_time_embedding(ops):
+    g = gen(44)
+    table = randn(g, 1000, 960, std=0.02)
+    ids = torch.randint(0, 1000, (2, 48), generator=g)
+    out = torch.zeros(2 * 241, 960, dtype=BF16, device="cuda")
+    # language rows 192..239 of each 241-row sample
+    ops.embed(ids.cuda(), table.cuda(), math.sqrt(960), out[192:], per_sample=48,
+              out_bs=241 * 960)
+    o = out.view(2, 241, 960).cpu()
+    torch.testing.assert_close(o[:, 192:240], ref.lang_embed(ids, table))
+    assert (o[:, :192] == 0).all() and (o[:, 240:] == 0).all()
+    bad = torch.tensor([5, -1, 1000], dtype=torch.int64)
+    ob = ops.embed(bad.cuda(), table.cuda(), 1.0, torch.ones(3, 960, dtype=BF16, device="cuda"))
+    assert (ob[1:] == 0).all()
+    for t in (1.0, 0.5, 0.1):
+        te = ops.time_embedding(t, 720).cpu()
+        want = ref.time_embedding(torch.tensor([t]), 720)[0].to(BF16)
+        torch.testing.assert_close(te.float(), want.float(), atol=1e-2, rtol=2 ** -7)
+
+
+def test_bad_shapes_raise(ops):
+    from smolvla._lib import SvlaError
+    a = torch.zeros(4, 12, dtype=BF16, device="cuda")            # K % 8 != 0
+    w = torch.zeros(8, 12, dtype=BF16, device="cuda")
+    with pytest.raises(SvlaError):
+        ops.linear(a, w)
+    q = torch.zeros(1, 4, 96, dtype=BF16, device="cuda")         # head_dim != 64 layout
+    with pytest.raises(SvlaError):
+        ops.attention(q, q, q, q, 2, 1)

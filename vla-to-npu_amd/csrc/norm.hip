@@ -1,0 +1,135 @@
+// Row normalisations (bandwidth-bound): one wave64 per row, 16-byte loads,
+// the row kept in registers (cols <= 2048), fp32 statistics with shuffle
+// reductions, one bf16 rounding of the output.
+//
+// RMSNorm replaces rms_norm_960_bf16 / rms_norm_bf16 (cc/bf16/rms_norm_960_bf16.cc:18-62,
+// cc/bf16_old/rms_norm_bf16.cc:16-64) and mirrors torch 2.10's nn.RMSNorm on
+// bf16 input: fp32 math x * rsqrt(mean(x^2) + eps) * w, one rounding.
+// LayerNorm replaces layer_norm_bf16 + its bias kernel
+// (cc/bf16_old/layer_norm_bf16.cc:16-70; vla/vision_block_bf16.py:101-127).
+#include "svla_common.h"
+
+namespace {
+
+constexpr int MAXC = 4;  // 16-byte chunks per lane: cols <= 4 * 8 * 64 = 2048
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16* __restrict__ x, long ldx,
+                                                      const bf16* __restrict__ w,
+                                                      bf16* __restrict__ y, long ldy, int rows,
+                                                      int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const bf16* xr = x + row * ldx;
+  bf16x8 v[MAXC];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = (lane + i * 64) * 8;
+    if (c < cols) {
+      v[i] = ld8(xr + c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float f = bf2f(v[i][j]);
+        ss += f * f;
+      }
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)cols + eps);
+  bf16* yr = y + row * ldy;
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = (lane + i * 64) * 8;
+    if (c < cols) {
+      const bf16x8 wv = ld8(w + c);
+      bf16x8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = f2bf(__fmul_rn(__fmul_rn(bf2f(v[i][j]), r), bf2f(wv[j])));
+      st8(yr + c, o);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void layernorm_kernel(const bf16* __restrict__ x, long ldx,
+                                                        const bf16* __restrict__ gmm,
+                                                        const bf16* __restrict__ bta,
+                                                        bf16* __restrict__ y, long ldy, int rows,
+                                                        int cols, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const bf16* xr = x + row * ldx;
+  bf16x8 v[MAXC];
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = (lane + i * 64) * 8;
+    if (c < cols) {
+      v[i] = ld8(xr + c);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += bf2f(v[i][j]);
+    }
+  }
+  const float mean = wave_sum(s) / (float)cols;
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = (lane + i * 64) * 8;
+    if (c < cols) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float d = bf2f(v[i][j]) - mean;
+        ss += d * d;
+      }
+    }
+  }
+  const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)cols + eps);
+  bf16* yr = y + row * ldy;
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = (lane + i * 64) * 8;
+    if (c < cols) {
+      const bf16x8 gv = ld8(gmm + c);
+      bf16x8 bv = bta ? ld8(bta + c) : bf16x8{};
+      bf16x8 o;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        o[j] = f2bf((bf2f(v[i][j]) - mean) * rstd * bf2f(gv[j]) + bf2f(bv[j]));
+      st8(yr + c, o);
+    }
+  }
+}
+
+bool norm_args_ok(const void* x, int ldx, const void* y, int ldy, int cols) {
+  return cols > 0 && cols % 8 == 0 && cols <= MAXC * 512 && ldx % 8 == 0 && ldy % 8 == 0 &&
+         ldx >= cols && ldy >= cols && svla_aligned16(x) && svla_aligned16(y);
+}
+
+}  // namespace
+
+extern "C" int svla_rmsnorm_bf16(const void* x, int ldx, const void* w, void* y, int ldy,
+                                 int rows, int cols, float eps, svla_stream_t stream) {
+  if (!norm_args_ok(x, ldx, y, ldy, cols) || !svla_aligned16(w) || rows < 0) return SVLA_EINVAL;
+  if (rows == 0) return SVLA_OK;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const bf16*>(x), (long)ldx, static_cast<const bf16*>(w),
+                     static_cast<bf16*>(y), (long)ldy, rows, cols, eps);
+  SVLA_CHECK_LAUNCH();
+  return SVLA_OK;
+}
+
+extern "C" int svla_layernorm_bf16(const void* x, int ldx, const void* gamma, const void* beta,
+                                   void* y, int ldy, int rows, int cols, float eps,
+                                   svla_stream_t stream) {
+  if (!norm_args_ok(x, ldx, y, ldy, cols) || !svla_aligned16(gamma) || rows < 0)
+    return SVLA_EINVAL;
+  if (beta && !svla_aligned16(beta)) return SVLA_EINVAL;
+  if (rows == 0) return SVLA_OK;
+  hipLaunchKernelGGL(layernorm_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const bf16*>(x), (long)ldx, static_cast<const bf16*>(gamma),
+                     static_cast<const bf16*>(beta), static_cast<bf16*>(y), (long)ldy, rows, cols,
+                     eps);
+  SVLA_CHECK_LAUNCH();
+  return SVLA_OK;
+}

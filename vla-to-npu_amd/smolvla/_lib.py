@@ -1,0 +1,79 @@
+"""ctypes binding of ``libsvla.so`` (the C-ABI declared in ``include/svla.h``).
+
+The library is the only compute path: there is no CPU fallback.  Loading
+fails loudly if the library has not been built.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "libsvla.so"
+
+_p = ctypes.c_void_p
+_i = ctypes.c_int
+_l = ctypes.c_long
+_f = ctypes.c_float
+_d = ctypes.c_double
+_fp = ctypes.POINTER(ctypes.c_float)
+
+# name -> argtypes (all return int)
+SIGNATURES = {
+    "svla_version": [],
+    "svla_rmsnorm_bf16": [_p, _i, _p, _p, _i, _i, _i, _f, _p],
+    "svla_layernorm_bf16": [_p, _i, _p, _p, _p, _i, _i, _i, _f, _p],
+    "svla_linear_bf16": [_p, _i, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _i, _i, _p, _l,
+                         _p],
+    "svla_linear_rope_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _l, _p],
+    "svla_linear_silu_mul_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _p, _l, _p],
+    "svla_patch_embed_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _l, _p],
+    "svla_connector_bf16": [_p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _l, _p],
+    "svla_action_out_euler": [_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _f, _p],
+    "svla_attention_bf16": [_p, _i, _l, _p, _i, _l, _p, _i, _l, _p, _i, _l, _i, _i, _i, _i, _i,
+                            _i, _f, _i, _i, _p],
+    "svla_masked_softmax_bf16": [_p, _i, _p, _i, _i, _p],
+    "svla_softmax": [_p, _p, _i, _i, _i, _i, _p],
+    "svla_silu_bf16": [_p, _p, _l, _p],
+    "svla_gelu_bf16": [_p, _p, _l, _i, _p],
+    "svla_silu_mul_bf16": [_p, _p, _p, _l, _p],
+    "svla_rope": [_p, _i, _p, _i, _i, _i, _p, _p, _i, _i, _i, _p],
+    "svla_rope_table": [_p, _p, _i, _i, _f, _p],
+    "svla_pack_weight_bf16": [_p, _i, _p, _i, _i, _p],
+    "svla_pack_gate_up_bf16": [_p, _p, _p, _i, _i, _p],
+    "svla_embed_bf16": [_p, _p, _l, _i, _f, _p, _i, _l, _l, _i, _p],
+    "svla_time_embedding_bf16": [_d, _i, _d, _d, _p, _p],
+    "svla_f32_to_bf16": [_p, _p, _l, _p],
+}
+
+_LIB = None
+
+
+def load(path: pathlib.Path = LIB_PATH):
+    """Load and type the library (cached)."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not path.exists():
+        raise RuntimeError(
+            f"{path} is not built; run `python -m smolvla.build` (or __graft_entry__.build()). "
+            "There is no CPU fallback for the SmolVLA kernels.")
+    lib = ctypes.CDLL(str(path))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_int
+    _LIB = lib
+    return lib
+
+
+class SvlaError(RuntimeError):
+    pass
+
+
+def call(name: str, *args):
+    rc = getattr(load(), name)(*args)
+    if rc != 0:
+        what = "invalid argument (shape / alignment)" if rc == -22 else f"HIP error {rc}"
+        raise SvlaError(f"{name}: {what}")
+    return rc

@@ -1,0 +1,267 @@
+"""PyTorch-facing wrappers over the C-ABI (device tensors in, device tensors out).
+
+Every function launches on ``torch.cuda.current_stream()`` and returns
+immediately (asynchronous, HIP-graph capturable).  Tensors must live on the
+GPU; 2-D operands may be row-strided views (``stride(-1) == 1``).  Linear
+weights are the packed ``[N, K]`` form made by :func:`pack_weight` /
+:func:`pack_gate_up`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+
+ACT = {None: 0, "none": 0, "gelu_tanh": 1, "tanh": 1, "gelu_erf": 2, "erf": 2, "silu": 3}
+MASK = {"none": 0, "causal": 1, "prefix_lm": 2}
+
+_WS = {}
+WS_BYTES = 64 << 20
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise ValueError("smolvla ops take GPU tensors (no CPU fallback)")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _ld(t):
+    if t.dim() != 2 or t.stride(-1) != 1:
+        raise ValueError(f"expected a row-major 2-D view, got shape {tuple(t.shape)} "
+                         f"strides {t.stride()}")
+    return t.stride(0)
+
+
+def workspace(device=None) -> torch.Tensor:
+    """Per-device fp32 split-K workspace (allocated once, reused)."""
+    dev = torch.device(device or torch.cuda.current_device())
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    ws = _WS.get(key)
+    if ws is None:
+        ws = torch.empty(WS_BYTES // 4, dtype=F32, device=dev)
+        _WS[key] = ws
+    return ws
+
+
+def _ws_args(ws):
+    if ws is False:
+        return None, 0
+    if ws is None:
+        ws = workspace()
+    return _ptr(ws), ws.numel() * 4
+
+
+# ----------------------------------------------------------------- norms ---
+def rmsnorm(x, w, eps, out=None):
+    eps = torch.finfo(F32).eps if eps is None else eps
+    rows, cols = x.shape
+    out = torch.empty(rows, cols, dtype=BF16, device=x.device) if out is None else out
+    _lib.call("svla_rmsnorm_bf16", _ptr(x), _ld(x), _ptr(w), _ptr(out), _ld(out), rows, cols,
+              float(eps), _stream())
+    return out
+
+
+def layernorm(x, g, b, eps, out=None):
+    rows, cols = x.shape
+    out = torch.empty(rows, cols, dtype=BF16, device=x.device) if out is None else out
+    _lib.call("svla_layernorm_bf16", _ptr(x), _ld(x), _ptr(g), _ptr(b), _ptr(out), _ld(out),
+              rows, cols, float(eps), _stream())
+    return out
+
+
+# ------------------------------------------------------------------ GEMM ---
+def linear(a, w, bias=None, bias_f32=None, res=None, act=None, alpha=1.0, out=None,
+           out_f32=False, ws=None):
+    """``epilogue(alpha * a @ w.T)``; ``w`` packed ``[N, K]``."""
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"linear: a {tuple(a.shape)} vs packed w {tuple(w.shape)}")
+    if out is None:
+        out = torch.empty(M, N, dtype=F32 if out_f32 else BF16, device=a.device)
+    wsp, wsb = _ws_args(ws)
+    _lib.call("svla_linear_bf16", _ptr(a), _ld(a), _ptr(w), _ld(w), _ptr(bias), _ptr(bias_f32),
+              _ptr(res), _ld(res) if res is not None else 0, _ptr(out), _ld(out), M, N, K,
+              float(alpha), ACT[act], int(out_f32), wsp, wsb, _stream())
+    return out
+
+
+def linear_rope(a, w, rope_cols, seq_len, cos_t, sin_t, out=None, ws=None):
+    M, K = a.shape
+    N = w.shape[0]
+    out = torch.empty(M, N, dtype=BF16, device=a.device) if out is None else out
+    wsp, wsb = _ws_args(ws)
+    _lib.call("svla_linear_rope_bf16", _ptr(a), _ld(a), _ptr(w), _ld(w), _ptr(out), _ld(out), M,
+              N, K, rope_cols, seq_len, _ptr(cos_t), _ptr(sin_t), wsp, wsb, _stream())
+    return out
+
+
+def linear_silu_mul(a, w_gu, out=None, ws=None):
+    M, K = a.shape
+    inter = w_gu.shape[0] // 2
+    out = torch.empty(M, inter, dtype=BF16, device=a.device) if out is None else out
+    wsp, wsb = _ws_args(ws)
+    _lib.call("svla_linear_silu_mul_bf16", _ptr(a), _ld(a), _ptr(w_gu), _ld(w_gu), _ptr(out),
+              _ld(out), M, inter, K, wsp, wsb, _stream())
+    return out
+
+
+def patch_embed(images, w, bias, pos, patch, out=None, ws=None):
+    """``images [n, C, H, H]`` bf16 contiguous; ``w [E, C*P*P]``."""
+    n, C, H, W = images.shape
+    E = w.shape[0]
+    G = H // patch
+    out = torch.empty(n * G * G, E, dtype=BF16, device=images.device) if out is None else out
+    wsp, wsb = _ws_args(ws)
+    _lib.call("svla_patch_embed_bf16", _ptr(images.contiguous()), _ptr(w), _ptr(bias), _ptr(pos),
+              _ptr(out), _ld(out), n, C, H, patch, E, wsp, wsb, _stream())
+    return out
+
+
+def connector(x, w, scale, out=None, ws=None):
+    """``x [n_img, grid*grid, hidden]`` contiguous -> ``[n_img*(grid/scale)^2, N]``."""
+    n, T, E = x.shape
+    grid = int(round(math.sqrt(T)))
+    N = w.shape[0]
+    rows = n * (grid // scale) ** 2
+    out = torch.empty(rows, N, dtype=BF16, device=x.device) if out is None else out
+    wsp, wsb = _ws_args(ws)
+    _lib.call("svla_connector_bf16", _ptr(x.contiguous()), _ptr(w), _ld(w), _ptr(out), _ld(out),
+              n, grid, E, scale, N, wsp, wsb, _stream())
+    return out
+
+
+def action_out_euler(a, w, x_f32, dt, x_bf16=None):
+    M, K = a.shape
+    N = w.shape[0]
+    _lib.call("svla_action_out_euler", _ptr(a), _ld(a), _ptr(w), _ld(w), _ptr(x_f32),
+              _ld(x_f32), _ptr(x_bf16), _ld(x_bf16) if x_bf16 is not None else 0, M, N, K,
+              float(dt), _stream())
+    return x_f32
+
+
+# ------------------------------------------------------------- attention ---
+def attention(q, k, v, out, hq, hkv, mask="causal", prefix_len=0, scale=None):
+    """``q [B, Sq, >=hq*64]``, ``k``/``v [B, Sk, >=hkv*64]`` (views into fused
+    projection buffers are fine: row stride = ``stride(1)``), ``out [B, Sq, hq*64]``."""
+    B, Sq = q.shape[0], q.shape[1]
+    Sk = k.shape[1]
+    for t in (q, k, v, out):
+        if t.dim() != 3 or t.stride(-1) != 1:
+            raise ValueError("attention takes [B, S, H*D] row-major views")
+    scale = 1.0 / math.sqrt(64) if scale is None else scale
+    _lib.call("svla_attention_bf16",
+              _ptr(q), q.stride(1), q.stride(0), _ptr(k), k.stride(1), k.stride(0),
+              _ptr(v), v.stride(1), v.stride(0), _ptr(out), out.stride(1), out.stride(0),
+              B, Sq, Sk, hq, hkv, 64, float(scale), MASK[mask], int(prefix_len), _stream())
+    return out
+
+
+# ------------------------------------------------------- harness kernels ---
+def masked_softmax(s, row_start, out=None):
+    rows, cols = s.shape
+    out = torch.empty(rows, cols, dtype=BF16, device=s.device) if out is None else out
+    _lib.call("svla_masked_softmax_bf16", _ptr(s.contiguous()), int(row_start), _ptr(out), rows,
+              cols, _stream())
+    return out
+
+
+def softmax(s, out=None, out_f32=False):
+    rows, cols = s.shape
+    if out is None:
+        out = torch.empty(rows, cols, dtype=F32 if out_f32 else BF16, device=s.device)
+    _lib.call("svla_softmax", _ptr(s.contiguous()), _ptr(out), rows, cols,
+              int(s.dtype == F32), int(out.dtype == F32), _stream())
+    return out
+
+
+def silu(x, out=None):
+    out = torch.empty_like(x) if out is None else out
+    _lib.call("svla_silu_bf16", _ptr(x.contiguous()), _ptr(out), x.numel(), _stream())
+    return out
+
+
+def gelu(x, kind="tanh", out=None):
+    out = torch.empty_like(x) if out is None else out
+    _lib.call("svla_gelu_bf16", _ptr(x.contiguous()), _ptr(out), x.numel(), ACT[kind], _stream())
+    return out
+
+
+def silu_mul(gate, up, out=None):
+    out = torch.empty_like(gate) if out is None else out
+    _lib.call("svla_silu_mul_bf16", _ptr(gate.contiguous()), _ptr(up.contiguous()), _ptr(out),
+              gate.numel(), _stream())
+    return out
+
+
+def rope(x, heads, cos_t, sin_t, pos_offset=0, out=None, out_f32=None):
+    rows = x.shape[0]
+    if out is None:
+        od = x.dtype if out_f32 is None else (F32 if out_f32 else BF16)
+        out = torch.empty(rows, x.shape[1], dtype=od, device=x.device)
+    _lib.call("svla_rope", _ptr(x), _ld(x), _ptr(out), _ld(out), rows, heads, _ptr(cos_t),
+              _ptr(sin_t), int(pos_offset), int(x.dtype == F32), int(out.dtype == F32),
+              _stream())
+    return out
+
+
+def rope_table(max_pos, head_dim, theta, device=None):
+    dev = device or torch.device("cuda")
+    c = torch.empty(max_pos, head_dim // 2, dtype=F32, device=dev)
+    s = torch.empty_like(c)
+    _lib.call("svla_rope_table", _ptr(c), _ptr(s), max_pos, head_dim, float(theta), _stream())
+    return c, s
+
+
+def pack_weight(w_kn, out=None):
+    """Reference ``[in, out]`` weight -> packed ``[out, in]`` on the device."""
+    K, N = w_kn.shape
+    out = torch.empty(N, K, dtype=BF16, device=w_kn.device) if out is None else out
+    _lib.call("svla_pack_weight_bf16", _ptr(w_kn), _ld(w_kn), _ptr(out), K, N, _stream())
+    return out
+
+
+def pack_gate_up(w_gate, w_up, out=None):
+    K, inter = w_gate.shape
+    out = torch.empty(2 * inter, K, dtype=BF16, device=w_gate.device) if out is None else out
+    _lib.call("svla_pack_gate_up_bf16", _ptr(w_gate.contiguous()), _ptr(w_up.contiguous()),
+              _ptr(out), K, inter, _stream())
+    return out
+
+
+def embed(ids, table, scale, out, per_sample=None, out_bs=0):
+    """Rows ``r`` of ``ids`` (flattened int64) -> ``out`` (2-D view with
+    leading dim), sample ``r // per_sample`` offset by ``out_bs`` elements."""
+    ids = ids.reshape(-1).to(torch.int64)
+    n = ids.numel()
+    per = n if per_sample is None else per_sample
+    _lib.call("svla_embed_bf16", _ptr(ids), _ptr(table), table.shape[0], table.shape[1],
+              float(scale), _ptr(out),
+              _ld(out), int(out_bs), n, per, _stream())
+    return out
+
+
+def time_embedding(t, dim, out=None, min_period=4e-3, max_period=4.0, device=None):
+    out = torch.empty(dim, dtype=BF16, device=device or "cuda") if out is None else out
+    _lib.call("svla_time_embedding_bf16", float(t), dim, float(min_period), float(max_period),
+              _ptr(out), _stream())
+    return out
+
+
+def f32_to_bf16(x, out=None):
+    out = torch.empty(x.shape, dtype=BF16, device=x.device) if out is None else out
+    _lib.call("svla_f32_to_bf16", _ptr(x), _ptr(out), x.numel(), _stream())
+    return out
