@@ -113,12 +113,16 @@ int svla_patch_embed_bf16(const void* images, const void* w, const void* bias, c
                           int embed, float* ws, long ws_bytes, svla_stream_t stream);
 
 /* Pixel-shuffle connector: out = pixel_shuffle(x, scale) . W^T with the shuffle
- * folded into the A-operand addressing.  x [n_img, grid*grid, hidden];
- * out rows are n_img*(grid/scale)^2, ldo.  Replaces connector_block/fused_op
- * (vla/connector_bf16.py:97-139; formula vla/vla.py:434-437). */
+ * folded into the A-operand addressing.  x [n_img, grid*grid, hidden]; the
+ * n_img*(grid/scale)^2 output rows are written with leading dim ldo, row m at
+ * (m / rows_per_sample) * sample_stride + m % rows_per_sample when
+ * rows_per_sample > 0 (e.g. 3 cameras x 64 tokens into each sample's 241-row
+ * prefix), contiguously when rows_per_sample == 0.  Replaces
+ * connector_block/fused_op (vla/connector_bf16.py:97-139; formula
+ * vla/vla.py:434-437). */
 int svla_connector_bf16(const void* x, const void* w, int ldw, void* out, int ldo, int n_img,
-                        int grid, int hidden, int scale, int n_out, float* ws, long ws_bytes,
-                        svla_stream_t stream);
+                        int grid, int hidden, int scale, int n_out, int rows_per_sample,
+                        int sample_stride, float* ws, long ws_bytes, svla_stream_t stream);
 
 /* Action output projection fused with the Euler update of the flow-matching
  * loop: v = bf16(A . W^T); x_f32 += dt * v; x_bf16 = bf16(x_f32) (x_bf16 may be

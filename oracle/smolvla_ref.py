@@ -313,7 +313,7 @@ def connector(x, w, scale: int):
 
 def lang_embed(ids, table):
     """``Embedding(ids) * sqrt(H)`` (vla/vla.py:169-174)."""
-    return (table[ids].float() * math.sqrt(table.shape[1])).to(BF16)
+    return (table[ids].float() * math.sqrt(table.shape[1])).to(table.dtype)
 
 
 def state_embed(state, w):
@@ -352,7 +352,8 @@ def build_prefix(vis, lang_ids, state, params, cfg):
     con = connector(vis.reshape(B * C, N, E), params["connector"]["W"], cfg.pixel_shuffle)
     con = con.reshape(B, C * con.shape[1], con.shape[2])
     lang = lang_embed(lang_ids, params["embed"])
-    st = state_embed(state.to(BF16)[:, None, :], params["state"]["W"])
+    wdt = params["state"]["W"].dtype
+    st = state_embed(state.to(wdt)[:, None, :], params["state"]["W"])
     return torch.cat([con, lang, st], dim=1)
 
 
@@ -387,8 +388,9 @@ def expert_input(x_t, t, params, cfg):
     io = params["expert_io"]
     B, L, _ = x_t.shape
     H = cfg.expert.hidden
-    a = linear(x_t.to(BF16), io["W_action_in"], io["b_action_in"])
-    te = time_embedding(torch.tensor([t]), H).to(BF16)
+    wdt = io["W_action_in"].dtype                       # bf16 (fp32 in pinning tests)
+    a = linear(x_t.to(wdt), io["W_action_in"], io["b_action_in"])
+    te = time_embedding(torch.tensor([t]), H).to(wdt)
     te = te[:, None, :].expand(B, L, H)
     h = linear(torch.cat([a, te], dim=2), io["W_time_in"], io["b_time_in"])
     return linear(silu(h), io["W_time_out"], io["b_time_out"])

@@ -60,12 +60,23 @@ struct GemmArgs {
   bf16* x_bf16;
   long ldxb;
   float dt;
+  // output row remap: row m is stored at (m / c_rpg) * c_gstride + m % c_rpg
+  // (c_rpg == 0: identity).  Lets the connector write each sample's image
+  // tokens straight into its slot of the [B, prefix_len, H] prefix buffer.
+  int c_rpg;
+  long c_gstride;
   // split-K
   float* ws;
   long ws_bytes;
   int splits;
   int kt_per_split;
 };
+
+__device__ __forceinline__ long crow(const GemmArgs& p, int m) {
+  if (p.c_rpg <= 0) return m;
+  const int g = m / p.c_rpg;
+  return (long)g * p.c_gstride + (m - g * p.c_rpg);
+}
 
 __device__ __forceinline__ float apply_act(int act, float v) {
   switch (act) {
@@ -88,7 +99,8 @@ __device__ __forceinline__ void load_bf16x4(const bf16* src, float v[4]) {
 }
 
 // ---- epilogues: each handles 4 consecutive columns of one row -------------
-// v already includes alpha.
+// v already includes alpha.  ACT is a compile-time activation (SVLA_ACT_*).
+template <int ACT>
 __device__ __forceinline__ void epi_store(const GemmArgs& p, int m, int n, float v[4]) {
   if (p.bias) {
     float b[4];
@@ -101,15 +113,15 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int m, int n, float
     for (int i = 0; i < 4; ++i) v[i] += p.bias_f32[n + i];
   }
   if (p.out_f32) {
-    float* dst = reinterpret_cast<float*>(p.c) + (long)m * p.ldc + n;
+    float* dst = reinterpret_cast<float*>(p.c) + crow(p, m) * p.ldc + n;
     *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
     return;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i) v[i] = rbf(v[i]);
-  if (p.act) {
+  if constexpr (ACT != SVLA_ACT_NONE) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = rbf(apply_act(p.act, v[i]));
+    for (int i = 0; i < 4; ++i) v[i] = rbf(apply_act(ACT, v[i]));
   }
   if (p.rowadd) {
     float r[4];
@@ -123,7 +135,7 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int m, int n, float
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = rbf(v[i] + r[i]);
   }
-  store_bf16x4(reinterpret_cast<bf16*>(p.c) + (long)m * p.ldc + n, v);
+  store_bf16x4(reinterpret_cast<bf16*>(p.c) + crow(p, m) * p.ldc + n, v);
 }
 
 // RoPE pair: x1 at columns n1..n1+3 (head dims d..d+3 < 32), x2 at n1+32.
@@ -131,7 +143,7 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int m, int n, float
 // out1 = x1*cos - x2*sin, out2 = x2*cos + x1*sin in fp32, then bf16.
 __device__ __forceinline__ void epi_rope(const GemmArgs& p, int m, int n1, float x1[4],
                                          float x2[4]) {
-  bf16* c = reinterpret_cast<bf16*>(p.c) + (long)m * p.ldc;
+  bf16* c = reinterpret_cast<bf16*>(p.c) + crow(p, m) * p.ldc;
 #pragma unroll
   for (int i = 0; i < 4; ++i) { x1[i] = rbf(x1[i]); x2[i] = rbf(x2[i]); }
   if (n1 < p.rope_cols) {
@@ -161,7 +173,7 @@ __device__ __forceinline__ void epi_silu(const GemmArgs& p, int m, int nout, flo
   float o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = rbf(silu_f(rbf(g[i]))) * rbf(u[i]);
-  store_bf16x4(reinterpret_cast<bf16*>(p.c) + (long)m * p.ldc + nout, o);
+  store_bf16x4(reinterpret_cast<bf16*>(p.c) + crow(p, m) * p.ldc + nout, o);
 }
 
 // Euler step x <- x + dt * bf16(v) in fp32 (+ optional bf16 copy of x).
@@ -214,7 +226,7 @@ __device__ __forceinline__ bf16x8 load_a(const GemmArgs& p, int m, int k) {
 constexpr int BK = 64;
 constexpr int LDS_STRIDE = BK + 8;  // elements; +16 bytes of padding per row
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int AMODE, int EPI>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int AMODE, int EPI, int ACT = SVLA_ACT_NONE>
 __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 16, TN = WN / 16;
@@ -370,7 +382,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
           if constexpr (EPI == EPI_EULER)
             epi_euler(p, m, n, v);
           else
-            epi_store(p, m, n, v);
+            epi_store<ACT>(p, m, n, v);
         }
       }
     }
@@ -378,7 +390,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
 }
 
 // Split-K reduction + epilogue.  One thread per epilogue unit.
-template <int EPI>
+template <int EPI, int ACT = SVLA_ACT_NONE>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p) {
   const long unit = (long)blockIdx.x * blockDim.x + threadIdx.x;
   const long MN = (long)p.M * p.N;
@@ -415,7 +427,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p) {
     const int m = unit / per_row, n = (unit - (long)m * per_row) * 4;
     float v[4];
     sum4(m, n, v);
-    epi_store(p, m, n, v);
+    epi_store<ACT>(p, m, n, v);
   }
 }
 
@@ -424,16 +436,33 @@ struct TileCfg {
   int bm, bn;
 };
 
-template <int AMODE, int EPI>
+template <int AMODE, int EPI, int ACT = SVLA_ACT_NONE>
 int launch_cfg(const TileCfg& t, dim3 grid, GemmArgs& p, hipStream_t s) {
   if (t.bm == 128)
-    hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, AMODE, EPI>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, AMODE, EPI, ACT>), grid, dim3(256), 0, s, p);
   else if (t.bm == 64 && t.bn == 128)
-    hipLaunchKernelGGL((gemm_kernel<64, 128, 2, 2, AMODE, EPI>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_kernel<64, 128, 2, 2, AMODE, EPI, ACT>), grid, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_kernel<64, 64, 4, 1, AMODE, EPI>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_kernel<64, 64, 4, 1, AMODE, EPI, ACT>), grid, dim3(256), 0, s, p);
   SVLA_CHECK_LAUNCH();
   return 0;
+}
+
+template <int EPI>
+void launch_reduce(int act, int blocks, GemmArgs& p, hipStream_t s) {
+  switch (act) {
+    case SVLA_ACT_GELU_TANH:
+      hipLaunchKernelGGL((splitk_reduce_kernel<EPI, SVLA_ACT_GELU_TANH>), dim3(blocks), dim3(256), 0, s, p);
+      break;
+    case SVLA_ACT_GELU_ERF:
+      hipLaunchKernelGGL((splitk_reduce_kernel<EPI, SVLA_ACT_GELU_ERF>), dim3(blocks), dim3(256), 0, s, p);
+      break;
+    case SVLA_ACT_SILU:
+      hipLaunchKernelGGL((splitk_reduce_kernel<EPI, SVLA_ACT_SILU>), dim3(blocks), dim3(256), 0, s, p);
+      break;
+    default:
+      hipLaunchKernelGGL((splitk_reduce_kernel<EPI, SVLA_ACT_NONE>), dim3(blocks), dim3(256), 0, s, p);
+  }
 }
 
 constexpr int kNumCU = 256;
@@ -454,6 +483,7 @@ int run_gemm(GemmArgs& p, int epi, hipStream_t s) {
   if (p.res && (p.ldr % 4)) return SVLA_EINVAL;
   if (epi == EPI_ROPE && (p.N % 64 || p.rope_cols % 64 || p.rope_period <= 0)) return SVLA_EINVAL;
   if (epi == EPI_SILU && p.N % 32) return SVLA_EINVAL;
+  if (AMODE != A_DENSE && p.act) return SVLA_EINVAL;
 
   TileCfg t = pick_tile(p.M, p.N);
   const int gm = (p.M + t.bm - 1) / t.bm, gn = (p.N + t.bn - 1) / t.bn;
@@ -488,7 +518,7 @@ int run_gemm(GemmArgs& p, int epi, hipStream_t s) {
     else if (epi == EPI_SILU)
       hipLaunchKernelGGL(splitk_reduce_kernel<EPI_SILU>, dim3(blocks), dim3(256), 0, s, p);
     else
-      hipLaunchKernelGGL(splitk_reduce_kernel<EPI_STORE>, dim3(blocks), dim3(256), 0, s, p);
+      launch_reduce<EPI_STORE>(p.act, blocks, p, s);
     SVLA_CHECK_LAUNCH();
     return 0;
   }
@@ -498,7 +528,13 @@ int run_gemm(GemmArgs& p, int epi, hipStream_t s) {
       case EPI_ROPE: return launch_cfg<AMODE, EPI_ROPE>(t, grid, p, s);
       case EPI_SILU: return launch_cfg<AMODE, EPI_SILU>(t, grid, p, s);
       case EPI_EULER: return launch_cfg<AMODE, EPI_EULER>(t, grid, p, s);
-      default: return launch_cfg<AMODE, EPI_STORE>(t, grid, p, s);
+      default:
+        switch (p.act) {
+          case SVLA_ACT_GELU_TANH: return launch_cfg<AMODE, EPI_STORE, SVLA_ACT_GELU_TANH>(t, grid, p, s);
+          case SVLA_ACT_GELU_ERF: return launch_cfg<AMODE, EPI_STORE, SVLA_ACT_GELU_ERF>(t, grid, p, s);
+          case SVLA_ACT_SILU: return launch_cfg<AMODE, EPI_STORE, SVLA_ACT_SILU>(t, grid, p, s);
+          default: return launch_cfg<AMODE, EPI_STORE>(t, grid, p, s);
+        }
     }
   } else {
     if (epi != EPI_STORE) return SVLA_EINVAL;
@@ -585,15 +621,19 @@ int svla_patch_embed_bf16(const void* images, const void* w, const void* bias, c
 }
 
 int svla_connector_bf16(const void* x, const void* w, int ldw, void* out, int ldo, int n_img,
-                        int grid, int hidden, int scale, int n_out, float* ws, long ws_bytes,
-                        svla_stream_t stream) {
+                        int grid, int hidden, int scale, int n_out, int rows_per_sample,
+                        int sample_stride, float* ws, long ws_bytes, svla_stream_t stream) {
   if (hidden % 8 || grid % scale || !svla_aligned16(x)) return SVLA_EINVAL;
+  if (rows_per_sample < 0 || (rows_per_sample > 0 && sample_stride < rows_per_sample))
+    return SVLA_EINVAL;
   const int gs = grid / scale;
   const int K = hidden * scale * scale;
   GemmArgs p = base_args(x, 0, w, ldw, out, ldo, n_img * gs * gs, n_out, K, ws, ws_bytes);
   p.g_grid = grid;
   p.g_hidden = hidden;
   p.g_scale = scale;
+  p.c_rpg = rows_per_sample;
+  p.c_gstride = sample_stride;
   return run_gemm<A_PSHUF>(p, EPI_STORE, (hipStream_t)stream);
 }
 

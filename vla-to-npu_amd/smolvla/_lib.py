@@ -28,7 +28,7 @@ SIGNATURES = {
     "svla_linear_rope_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _l, _p],
     "svla_linear_silu_mul_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _p, _l, _p],
     "svla_patch_embed_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _l, _p],
-    "svla_connector_bf16": [_p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _l, _p],
+    "svla_connector_bf16": [_p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _l, _p],
     "svla_action_out_euler": [_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _f, _p],
     "svla_attention_bf16": [_p, _i, _l, _p, _i, _l, _p, _i, _l, _p, _i, _l, _i, _i, _i, _i, _i,
                             _i, _f, _i, _i, _p],

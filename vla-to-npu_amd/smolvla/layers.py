@@ -1,0 +1,186 @@
+"""GPU transformer layers built from the C-ABI kernels.
+
+Weights are prepared once into the packed layouts the kernels consume
+(``prep_*``), then each layer is a short, fixed sequence of launches on the
+current stream, writing into caller-provided buffers so a whole chunk can be
+captured in one HIP graph.  Activations are row-major ``[B*S, H]`` bf16.
+
+Per decoder layer (vla/text_encoder_bf16.py:480-595 -> 7 launches):
+  rmsnorm -> QKV GEMM with RoPE epilogue -> fused GQA attention ->
+  O GEMM + residual -> rmsnorm -> gate|up GEMM with SiLU*up epilogue ->
+  down GEMM + residual.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import ops
+from .config import DecoderConfig, VitConfig, resolve_eps
+
+BF16 = torch.bfloat16
+
+
+# ------------------------------------------------------------ weight prep ---
+def _dev(t, device):
+    return t.to(device=device, dtype=BF16).contiguous()
+
+
+def _pack_cols(ws, device):
+    """Pack ``[K, N_i]`` reference weights side by side into one ``[sum N_i, K]``."""
+    K = ws[0].shape[0]
+    out = torch.empty(sum(w.shape[1] for w in ws), K, dtype=BF16, device=device)
+    r = 0
+    for w in ws:
+        ops.pack_weight(_dev(w, device), out=out[r:r + w.shape[1]])
+        r += w.shape[1]
+    return out
+
+
+def prep_decoder(p, device):
+    """SmolLM2 decoder / expert self layer: fused QKV [q|k|v, H], O, gate|up, down."""
+    return dict(
+        wqkv=_pack_cols([p["Wq"], p["Wk"], p["Wv"]], device),
+        wo=ops.pack_weight(_dev(p["Wo"], device)),
+        wgu=ops.pack_gate_up(_dev(p["W_gate"], device), _dev(p["W_up"], device)),
+        wd=ops.pack_weight(_dev(p["W_down"], device)),
+        n1=_dev(p["W_norm_1"], device), n2=_dev(p["W_norm_2"], device),
+    )
+
+
+def prep_cross(p, device):
+    """Expert cross layer: Q, the cross K/V projections, O, gate|up, down."""
+    return dict(
+        wq=ops.pack_weight(_dev(p["Wq"], device)),
+        wkc=ops.pack_weight(_dev(p["Wk_cross"], device)),
+        wvc=ops.pack_weight(_dev(p["Wv_cross"], device)),
+        wo=ops.pack_weight(_dev(p["Wo"], device)),
+        wgu=ops.pack_gate_up(_dev(p["W_gate"], device), _dev(p["W_up"], device)),
+        wd=ops.pack_weight(_dev(p["W_down"], device)),
+        n1=_dev(p["W_norm_1"], device), n2=_dev(p["W_norm_2"], device),
+    )
+
+
+def prep_vit(p, device):
+    H = p["Wq"].shape[0]
+    bqkv = None
+    if p.get("bq") is not None:
+        bqkv = torch.empty(3 * H, dtype=BF16, device=device)
+        for i, k in enumerate(("bq", "bk", "bv")):
+            bqkv[i * H:(i + 1) * H].copy_(p[k])
+    opt = lambda k: _dev(p[k], device) if p.get(k) is not None else None  # noqa: E731
+    return dict(
+        wqkv=_pack_cols([p["Wq"], p["Wk"], p["Wv"]], device), bqkv=bqkv,
+        wo=ops.pack_weight(_dev(p["Wo"], device)), bo=opt("bo"),
+        wup=ops.pack_weight(_dev(p["W_up"], device)), bup=opt("b_up"),
+        wd=ops.pack_weight(_dev(p["W_down"], device)), bd=opt("b_down"),
+        g1=_dev(p["W_norm_1"], device), b1=opt("b_norm_1"),
+        g2=_dev(p["W_norm_2"], device), b2=opt("b_norm_2"),
+    )
+
+
+@dataclass
+class Rope:
+    cos: torch.Tensor
+    sin: torch.Tensor
+    seq_len: int
+
+    @classmethod
+    def make(cls, seq_len, head_dim, theta, device):
+        c, s = ops.rope_table(seq_len, head_dim, theta, device=device)
+        return cls(c, s, seq_len)
+
+
+class Buffers:
+    """Lazily allocated, reusable activation buffers keyed by name."""
+
+    def __init__(self, device):
+        self.device = device
+        self._b = {}
+
+    def get(self, name, rows, cols, dtype=BF16):
+        t = self._b.get(name)
+        if t is None or t.shape[0] < rows or t.shape[1] != cols or t.dtype != dtype:
+            t = torch.empty(rows, cols, dtype=dtype, device=self.device)
+            self._b[name] = t
+        return t[:rows]
+
+
+# ----------------------------------------------------------------- layers ---
+def decoder_layer(x, P, cfg: DecoderConfig, B, L, rope: Rope, mask="causal", prefix_len=0,
+                  bufs: Optional[Buffers] = None, qkv_out=None, ws=None, mid_out=None):
+    """One SmolLM2-style block on ``x [B*L, H]`` **in place**; returns the
+    fused projection buffer ``[B*L, q|k|v]`` whose K (post-RoPE) and V column
+    slices are this layer's KV cache (vla/text_encoder_bf16.py:480-595).
+    ``mid_out`` (optional) receives the mid-block residual (after attention)."""
+    bufs = bufs or Buffers(x.device)
+    M = B * L
+    qd, kvd = cfg.q_dim, cfg.kv_dim
+    eps = resolve_eps(cfg.rms_eps)
+    h = ops.rmsnorm(x, P["n1"], eps, out=bufs.get("h", M, cfg.hidden))
+    qkv = qkv_out if qkv_out is not None else bufs.get("qkv", M, qd + 2 * kvd)
+    ops.linear_rope(h, P["wqkv"], qd + kvd, L, rope.cos, rope.sin, out=qkv, ws=ws)
+    q3 = qkv.view(B, L, -1)
+    attn = bufs.get("attn", M, qd)
+    ops.attention(q3[:, :, :qd], q3[:, :, qd:qd + kvd], q3[:, :, qd + kvd:],
+                  attn.view(B, L, qd), cfg.n_q_heads, cfg.n_kv_heads, mask, prefix_len)
+    ops.linear(attn, P["wo"], res=x, out=x, ws=ws)
+    if mid_out is not None:
+        mid_out.copy_(x)
+    _mlp(x, P, cfg, M, eps, bufs, ws)
+    return qkv
+
+
+def _mlp(x, P, cfg, M, eps, bufs, ws):
+    h = ops.rmsnorm(x, P["n2"], eps, out=bufs.get("h", M, cfg.hidden))
+    act = ops.linear_silu_mul(h, P["wgu"], out=bufs.get("mlp", M, cfg.inter), ws=ws)
+    ops.linear(act, P["wd"], res=x, out=x, ws=ws)
+
+
+def cross_kv(k_src, v_src, P, out_k=None, out_v=None, ws=None):
+    """Cross-attention K/V projections of the prefix cache
+    (vla/action_expert_bf16.py:757-758)."""
+    k = ops.linear(k_src, P["wkc"], out=out_k, ws=ws)
+    v = ops.linear(v_src, P["wvc"], out=out_v, ws=ws)
+    return k, v
+
+
+def cross_layer(x, ck, cv, P, cfg: DecoderConfig, B, L, Lc, rope: Rope,
+                bufs: Optional[Buffers] = None, ws=None):
+    """Expert cross-attention block on ``x [B*L, H]`` in place, attending to
+    the already projected ``ck``/``cv [B*Lc, kv]`` (vla/action_expert_bf16.py:731-803;
+    RoPE on Q only, no mask)."""
+    bufs = bufs or Buffers(x.device)
+    M = B * L
+    qd = cfg.q_dim
+    eps = resolve_eps(cfg.rms_eps)
+    h = ops.rmsnorm(x, P["n1"], eps, out=bufs.get("h", M, cfg.hidden))
+    q = ops.linear_rope(h, P["wq"], qd, L, rope.cos, rope.sin, out=bufs.get("q", M, qd), ws=ws)
+    attn = bufs.get("attn", M, qd)
+    ops.attention(q.view(B, L, qd), ck.view(B, Lc, -1), cv.view(B, Lc, -1), attn.view(B, L, qd),
+                  cfg.n_q_heads, cfg.n_kv_heads, "none", 0)
+    ops.linear(attn, P["wo"], res=x, out=x, ws=ws)
+    _mlp(x, P, cfg, M, eps, bufs, ws)
+
+
+def vit_layer(x, P, cfg: VitConfig, n_img, T, bufs: Optional[Buffers] = None, ws=None):
+    """SigLIP-style block on ``x [n_img*T, H]`` in place
+    (vla/vision_block_bf16.py:308-420)."""
+    bufs = bufs or Buffers(x.device)
+    M = n_img * T
+    H = cfg.hidden
+    h = ops.layernorm(x, P["g1"], P["b1"], cfg.ln_eps, out=bufs.get("vh", M, H))
+    qkv = ops.linear(h, P["wqkv"], bias=P["bqkv"], out=bufs.get("vqkv", M, 3 * H), ws=ws)
+    q3 = qkv.view(n_img, T, 3 * H)
+    attn = bufs.get("vattn", M, H)
+    ops.attention(q3[:, :, :H], q3[:, :, H:2 * H], q3[:, :, 2 * H:], attn.view(n_img, T, H),
+                  cfg.n_heads, cfg.n_heads, "none", 0, scale=1.0 / math.sqrt(cfg.head_dim))
+    ops.linear(attn, P["wo"], bias=P["bo"], res=x, out=x, ws=ws)
+    h = ops.layernorm(x, P["g2"], P["b2"], cfg.ln_eps, out=bufs.get("vh", M, H))
+    act = ops.linear(h, P["wup"], bias=P["bup"], act="gelu_" + cfg.gelu,
+                     out=bufs.get("vmlp", M, cfg.inter), ws=ws)
+    ops.linear(act, P["wd"], bias=P["bd"], res=x, out=x, ws=ws)

@@ -131,16 +131,22 @@ def patch_embed(images, w, bias, pos, patch, out=None, ws=None):
     return out
 
 
-def connector(x, w, scale, out=None, ws=None):
-    """``x [n_img, grid*grid, hidden]`` contiguous -> ``[n_img*(grid/scale)^2, N]``."""
+def connector(x, w, scale, out=None, rows_per_sample=0, sample_stride=0, ws=None):
+    """``x [n_img, grid*grid, hidden]`` contiguous -> ``[n_img*(grid/scale)^2, N]``
+    (or remapped into a larger buffer, see ``svla_connector_bf16``)."""
     n, T, E = x.shape
     grid = int(round(math.sqrt(T)))
     N = w.shape[0]
     rows = n * (grid // scale) ** 2
     out = torch.empty(rows, N, dtype=BF16, device=x.device) if out is None else out
+    if rows_per_sample:
+        need = (rows // rows_per_sample - 1) * sample_stride + rows_per_sample
+        if out.shape[0] < need:
+            raise ValueError("connector: output buffer too small for the row remap")
     wsp, wsb = _ws_args(ws)
     _lib.call("svla_connector_bf16", _ptr(x.contiguous()), _ptr(w), _ld(w), _ptr(out), _ld(out),
-              n, grid, E, scale, N, wsp, wsb, _stream())
+              n, grid, E, scale, N, int(rows_per_sample), int(sample_stride), wsp, wsb,
+              _stream())
     return out
 
 
