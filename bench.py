@@ -92,13 +92,13 @@ def dominant_kernel_roofline(eng, iters):
     x = eng.vbufs.get("vh", M, v.hidden)
     out = eng.vbufs.get("vmlp", M, v.inter)
     for _ in range(3):
-        ops.linear(x, P["wup"], bias=P["bup"], act="gelu_" + v.gelu, out=out, ws=eng.ws)
+        ops.linear(x, P["wup"], bias=P["bup"], act="gelu_" + v.gelu, out=out)
     torch.cuda.synchronize()
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(iters):
-        ops.linear(x, P["wup"], bias=P["bup"], act="gelu_" + v.gelu, out=out, ws=eng.ws)
+        ops.linear(x, P["wup"], bias=P["bup"], act="gelu_" + v.gelu, out=out)
     b.record()
     b.synchronize()
     avg_ms = a.elapsed_time(b) / iters

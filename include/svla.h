@@ -68,40 +68,52 @@ int svla_layernorm_bf16(const void* x, int ldx, const void* gamma, const void* b
                         int ldy, int rows, int cols, float eps, svla_stream_t stream);
 
 /* ----------------------------------------------------------------- GEMM --
- * C[M,N] = epilogue(alpha * A[M,K] . W[N,K]^T) on bf16 MFMA (fp32 accumulate).
+ * C[M,N] = epilogue(alpha * norm(A)[M,K] . W[N,K]^T) on bf16 MFMA (fp32 accumulate).
  * Replaces the Allo GEMM module GEMM(M,N,K,Pm,Pn,Pk,bf16,bf16) and its K-chunk
  * host accumulation (vla/text_encoder_bf16.py:174-225, 584-590; contract
  * cc/gemm.py:44-77), the attention-score kernel transpose_matmul_with_scale_bf16
  * (cc/bf16_old/transpose_matmul_with_scale_bf16.cc:52, alpha = 0.125) and the
  * residual adds (vla/text_encoder_bf16.py:532,592).
+ * norm_w (may be NULL): the A rows are RMS-normalised on the fly,
+ *   A[m,k] = bf16(x[m,k] * rsqrt(mean_k(x[m,:]^2) + norm_eps) * norm_w[k])
+ * (the rmsnorm() that precedes every projection, vla/text_encoder_bf16.py:398-404).
  * Epilogue order (mirrors the torch modules' bf16 boundaries):
  *   v = alpha*acc (+ bias[n]) (+ bias_f32[n]); if out_f32: store fp32 v.
  *   else v = bf16(v); v = bf16(act(v)); if res: v = bf16(v + res[m,n]); store.
- * bias/bias_f32/res may be NULL.  K % 8 == 0, N % 4 == 0, aligned.
- * `ws` is an fp32 workspace for split-K (may be NULL: no split), `ws_bytes`
- * its size; the library picks a split count that fits. */
+ * bias/bias_f32/res may be NULL; res may alias c (in-place residual update).
+ * K % 8 == 0, N % 4 == 0, aligned.  No workspace: problems with few rows
+ * (M <= 256) split K across the waves of each workgroup instead of across
+ * workgroups. */
 int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
                      const float* bias_f32, const void* res, int ldr, void* c, int ldc, int m,
-                     int n, int k, float alpha, int act, int out_f32, float* ws, long ws_bytes,
-                     svla_stream_t stream);
+                     int n, int k, float alpha, int act, int out_f32, const void* norm_w,
+                     float norm_eps, svla_stream_t stream);
 
-/* Fused QKV projection with rotate-half RoPE in the epilogue.
+/* Tuning hook: force the GEMM tile configuration for every later call
+ * (0: 256x256/32x32-MFMA, 1: 128x128/32x32, 2: 64x128/16x16, 3: 64x64/16x16,
+ * 4: skinny 64x64, 5: skinny 64x32, 6: 128x128/16x16), or -1 for the automatic
+ * shape-based choice (default).  Process-wide; not thread-safe. */
+int svla_gemm_set_tile(int tile);
+
+/* Fused (RMSNorm +) QKV projection with rotate-half RoPE in the epilogue.
  * Columns [0, rope_cols) are heads of 64 that get RoPE at position
  * (row % seq_len) with fp32 tables cos/sin [seq_len, 32]; the remaining columns
- * (V) are stored as projected.  Replaces gemm_q/gemm_kv + rope_apply_packed
- * (vla/text_encoder_bf16.py:422-475, 491-500; kernels cc/float/rope_vec_ops.cc,
- * sine.cc, cosine.cc).  rope_cols % 64 == 0. */
+ * (V) are stored as projected.  Replaces rmsnorm + gemm_q/gemm_kv +
+ * rope_apply_packed (vla/text_encoder_bf16.py:422-475, 486-500; kernels
+ * cc/float/rope_vec_ops.cc, sine.cc, cosine.cc).  n % 64 == 0, rope_cols % 64 == 0. */
 int svla_linear_rope_bf16(const void* a, int lda, const void* w, int ldw, void* c, int ldc,
                           int m, int n, int k, int rope_cols, int seq_len, const float* cos_t,
-                          const float* sin_t, float* ws, long ws_bytes, svla_stream_t stream);
+                          const float* sin_t, const void* norm_w, float norm_eps,
+                          svla_stream_t stream);
 
-/* Gated MLP up-projection: out[M, inter] = bf16(silu(gate) ) * bf16(up), gate/up
- * from one GEMM over the interleaved weight produced by svla_pack_gate_up_bf16.
- * Replaces gemm_ffn_up x2 + silu_*_bf16 + the numpy hadamard
- * (vla/text_encoder_bf16.py:537-581; vla/action_expert_bf16.py:629-642). */
+/* Gated MLP up-projection: out[M, inter] = bf16(silu(gate)) * bf16(up) (bf16),
+ * gate/up from one GEMM over the weight interleaved by svla_pack_gate_up_bf16
+ * (optionally on RMS-normalised A).  Replaces rmsnorm + gemm_ffn_up x2 +
+ * silu_*_bf16 + the numpy hadamard (vla/text_encoder_bf16.py:534-581;
+ * vla/action_expert_bf16.py:629-642).  inter % 32 == 0. */
 int svla_linear_silu_mul_bf16(const void* a, int lda, const void* w_gu, int ldw, void* out,
-                              int ldo, int m, int inter, int k, float* ws, long ws_bytes,
-                              svla_stream_t stream);
+                              int ldo, int m, int inter, int k, const void* norm_w,
+                              float norm_eps, svla_stream_t stream);
 
 /* Patch embedding: Conv2d(C -> E, kernel = stride = P) as an im2col GEMM over
  * images [n_img, C, H, H] bf16, + conv bias, + learned position embedding
@@ -110,7 +122,7 @@ int svla_linear_silu_mul_bf16(const void* a, int lda, const void* w_gu, int ldw,
  * cc/bf16_old/conv_bf16.cc:12) + the position add (vla/vit_emb.py:43-47). */
 int svla_patch_embed_bf16(const void* images, const void* w, const void* bias, const void* pos,
                           void* out, int ldo, int n_img, int chans, int image, int patch,
-                          int embed, float* ws, long ws_bytes, svla_stream_t stream);
+                          int embed, svla_stream_t stream);
 
 /* Pixel-shuffle connector: out = pixel_shuffle(x, scale) . W^T with the shuffle
  * folded into the A-operand addressing.  x [n_img, grid*grid, hidden]; the
@@ -122,15 +134,16 @@ int svla_patch_embed_bf16(const void* images, const void* w, const void* bias, c
  * vla/vla.py:434-437). */
 int svla_connector_bf16(const void* x, const void* w, int ldw, void* out, int ldo, int n_img,
                         int grid, int hidden, int scale, int n_out, int rows_per_sample,
-                        int sample_stride, float* ws, long ws_bytes, svla_stream_t stream);
+                        int sample_stride, svla_stream_t stream);
 
-/* Action output projection fused with the Euler update of the flow-matching
- * loop: v = bf16(A . W^T); x_f32 += dt * v; x_bf16 = bf16(x_f32) (x_bf16 may be
- * NULL).  Replaces postprocessing's GEMM (vla/vla.py:218-222) and adds the
- * update the reference lacks. */
+/* Action output projection fused with the final expert RMSNorm (norm_w, may
+ * be NULL) and the Euler update of the flow-matching loop:
+ * v = bf16(norm(A) . W^T); x_f32 += dt * v; x_bf16 = bf16(x_f32) (x_bf16 may be
+ * NULL).  Replaces postprocessing's RMSNorm + GEMM (vla/vla.py:218-222) and adds
+ * the update the reference lacks. */
 int svla_action_out_euler(const void* a, int lda, const void* w, int ldw, float* x_f32,
-                          int ldx, void* x_bf16, int ldxb, int m, int n, int k, float dt,
-                          svla_stream_t stream);
+                          int ldx, void* x_bf16, int ldxb, int m, int n, int k,
+                          const void* norm_w, float norm_eps, float dt, svla_stream_t stream);
 
 /* ------------------------------------------------------------ attention --
  * Fused GQA attention: O = softmax(scale * Q K^T + mask) V per head, query
@@ -195,8 +208,8 @@ int svla_pack_weight_bf16(const void* w_kn, int ldw, void* out_nk, int k, int n,
                           svla_stream_t stream);
 
 /* Interleave gate/up weights ([K, inter] each, reference layout) into the
- * [2*inter, K] layout consumed by svla_linear_silu_mul_bf16 (blocks of 16 rows
- * alternating gate/up).  inter % 16 == 0. */
+ * [2*inter, K] layout consumed by svla_linear_silu_mul_bf16 (blocks of 32 rows
+ * alternating gate/up).  inter % 32 == 0. */
 int svla_pack_gate_up_bf16(const void* w_gate, const void* w_up, void* out, int k, int inter,
                            svla_stream_t stream);
 

@@ -15,7 +15,7 @@ HEADER = ROOT / "include" / "svla.h"
 def declared_symbols():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\bint\s+(svla_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(?:int|long)\s+(svla_\w+)\s*\(", text)))
 
 
 def test_header_declares_entry_points():
@@ -37,7 +37,7 @@ def test_ctypes_table_matches_header():
     from smolvla import _lib
     assert sorted(_lib.SIGNATURES) == declared_symbols()
     lib = _lib.load()
-    assert lib.svla_version() == 100
+    assert lib.svla_version() == 200
 
 
 def test_ops_refuse_cpu_tensors():

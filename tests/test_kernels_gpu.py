@@ -88,21 +88,23 @@ def test_layernorm(ops, rows, cols):
 
 # ------------------------------------------------------------------- GEMM ---
 GEMM_SHAPES = [
+    # small-M (64x64 / 64x128 tiles, 16x16x32 MFMA, split-K)
     (1, 32, 32), (50, 960, 720), (50, 720, 960), (50, 32, 720), (128, 960, 960),
     (241, 1600, 960), (241, 960, 2560), (192, 960, 12288), (1024, 2304, 768),
     (1024, 768, 3072), (3, 720, 1440), (77, 100, 24),
+    # 128x128 and 256x256 tiles (32x32x16 MFMA)
+    (4096, 1024, 256), (7712, 960, 960), (8192, 2304, 768), (9000, 772, 200),
 ]
 
 
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
-@pytest.mark.parametrize("split", [True, False])
-def test_linear(ops, M, N, K, split):
+def test_linear(ops, M, N, K):
     g = gen(M * 7 + N + K)
     a = randn(g, M, K)
     w = randn(g, K, N, std=0.02)
     wp = ops.pack_weight(w.cuda())
     torch.testing.assert_close(wp.cpu(), w.t().contiguous())
-    got = ops.linear(a.cuda(), wp, ws=None if split else False)
+    got = ops.linear(a.cuda(), wp)
     want = ref.linear(a, w)
     assert_close_bf16(got, want)
 
@@ -119,12 +121,69 @@ def test_linear_bias_act_residual(ops):
     got = ops.linear(a.cuda(), wp, bias=b.cuda(), res=res.cuda())
     want = ref.linear(a, w, b) + res
     assert_close_bf16(got, want)
-    got = ops.linear(a.cuda(), wp, act="silu", ws=False)
+    got = ops.linear(a.cuda(), wp, act="silu")
     assert_close_bf16(got, ref.silu(ref.linear(a, w)))
     bf = torch.randn(N, generator=g) * 0.1
     got = ops.linear(a.cuda(), wp, bias_f32=bf.cuda(), out_f32=True)
     want = a.float() @ w.float() + bf
     assert rel_err(got, want) < 1e-3
+
+
+def test_linear_gelu_big_tile(ops):
+    # the ViT MLP up-projection shape class on the 256x256 tile
+    g = gen(13)
+    M, N, K = 8192, 3072, 768
+    a, w, b = randn(g, M, K), randn(g, K, N, std=0.02), randn(g, N, std=0.02)
+    got = ops.linear(a.cuda(), ops.pack_weight(w.cuda()), bias=b.cuda(), act="gelu_tanh")
+    assert_close_bf16(got, ref.gelu(ref.linear(a, w, b), "tanh"))
+
+
+@pytest.mark.parametrize("M,K", [(50, 720), (241, 960), (7712, 960), (3, 2048)])
+def test_fused_rmsnorm_prologue(ops, M, K):
+    """norm=(w, eps): A rows RMS-normalised inside the GEMM ~= rmsnorm then GEMM."""
+    g = gen(M + K + 1)
+    x = randn(g, M, K, std=2.0)
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16)
+    w = randn(g, K, 1600, std=0.02)
+    wp = ops.pack_weight(w.cuda())
+    h = ref.rms_norm(x, nw, 1e-5)
+    got = ops.linear(x.cuda(), wp, norm=(nw.cuda(), 1e-5))
+    assert_close_bf16(got, ref.linear(h, w))
+    # vs the standalone RMSNorm kernel followed by the GEMM: the row statistics
+    # are summed in a different fp32 order, so last-bit flips of the normalised
+    # bf16 operand are allowed: outputs agree to within 2^-6 of their range
+    def same(a, b):
+        assert_close_bf16(a, b)
+        assert rel_err(a, b) <= 2 ** -6
+
+    sep = ops.linear(ops.rmsnorm(x.cuda(), nw.cuda(), 1e-5), wp)
+    same(got, sep)
+    c, s_ = ops.rope_table(50, 64, 1e5)
+    if M % 50 == 0:
+        got = ops.linear_rope(x.cuda(), wp, 1280, 50, c, s_, norm=(nw.cuda(), 1e-5))
+        sep = ops.linear_rope(ops.rmsnorm(x.cuda(), nw.cuda(), 1e-5), wp, 1280, 50, c, s_)
+        same(got, sep)
+    wg, wu = randn(g, K, 2048, std=0.02), randn(g, K, 2048, std=0.02)
+    wgu = ops.pack_gate_up(wg.cuda(), wu.cuda())
+    got = ops.linear_silu_mul(x.cuda(), wgu, norm=(nw.cuda(), 1e-5))
+    sep = ops.linear_silu_mul(ops.rmsnorm(x.cuda(), nw.cuda(), 1e-5), wgu)
+    same(got, sep)
+
+
+def test_repeated_calls_deterministic(ops):
+    """Skinny-M calls of different shapes back to back: each result is
+    correct and bit-identical across repetitions (no cross-call state)."""
+    g = gen(14)
+    cases = []
+    for (M, N, K) in ((50, 960, 720), (50, 720, 2048), (241, 320, 320), (50, 960, 720)):
+        a, w = randn(g, M, K), randn(g, K, N, std=0.02)
+        cases.append((a.cuda(), ops.pack_weight(w.cuda()), ref.linear(a, w)))
+    first = [ops.linear(a, wp) for a, wp, _ in cases]
+    for rep in range(3):
+        for (a, wp, want), f in zip(cases, first):
+            got = ops.linear(a, wp)
+            assert_close_bf16(got, want)
+            assert torch.equal(got, f)
 
 
 def test_linear_alpha_attn_score_harness(ops):
@@ -140,10 +199,10 @@ def test_linear_alpha_attn_score_harness(ops):
         torch.testing.assert_close(C.cpu().float(), want.float(), atol=1e-1, rtol=1e-2)
 
 
-@pytest.mark.parametrize("M,L,hid,split", [(128, 128, 960, True), (241, 241, 960, False),
-                                           (482, 241, 960, True), (50, 50, 720, True),
-                                           (100, 50, 720, False)])
-def test_linear_rope_qkv(ops, M, L, hid, split):
+@pytest.mark.parametrize("M,L,hid", [(128, 128, 960), (241, 241, 960), (482, 241, 960),
+                                     (50, 50, 720), (100, 50, 720), (7712, 241, 960),
+                                     (16384, 128, 960)])
+def test_linear_rope_qkv(ops, M, L, hid):
     g = gen(M + hid)
     theta = 100000.0
     x = randn(g, M, hid)
@@ -155,8 +214,7 @@ def test_linear_rope_qkv(ops, M, L, hid, split):
     # angles reach ~240 rad: a 1-2 ulp fp32 difference in the angle (powf) is ~4e-6
     torch.testing.assert_close(cos_t.cpu(), c_ref, atol=1e-5, rtol=0)
     torch.testing.assert_close(sin_t.cpu(), s_ref, atol=1e-5, rtol=0)
-    got = ops.linear_rope(x.cuda(), ops.pack_weight(w.cuda()), 1280, L, cos_t, sin_t,
-                          ws=None if split else False).cpu()
+    got = ops.linear_rope(x.cuda(), ops.pack_weight(w.cuda()), 1280, L, cos_t, sin_t).cpu()
     B = M // L
     q = ref.apply_rope(ref.linear(x, wq).view(B, L, 15, 64), theta).to(BF16).view(M, 960)
     k = ref.apply_rope(ref.linear(x, wk).view(B, L, 5, 64), theta).to(BF16).view(M, 320)
@@ -166,14 +224,14 @@ def test_linear_rope_qkv(ops, M, L, hid, split):
     assert_close_bf16(got[:, 1280:], v)
 
 
-@pytest.mark.parametrize("M,K,inter,split", [(50, 720, 2048, True), (241, 960, 2560, False),
-                                             (1024, 960, 2560, True), (5, 64, 48, False)])
-def test_linear_silu_mul(ops, M, K, inter, split):
+@pytest.mark.parametrize("M,K,inter", [(50, 720, 2048), (241, 960, 2560), (1024, 960, 2560),
+                                       (5, 64, 64), (7712, 960, 2560), (3000, 720, 2048)])
+def test_linear_silu_mul(ops, M, K, inter):
     g = gen(M + K)
     x = randn(g, M, K)
     wg, wu = randn(g, K, inter, std=0.02), randn(g, K, inter, std=0.02)
     wgu = ops.pack_gate_up(wg.cuda(), wu.cuda())
-    got = ops.linear_silu_mul(x.cuda(), wgu, ws=None if split else False)
+    got = ops.linear_silu_mul(x.cuda(), wgu)
     want = ref.silu(ref.linear(x, wg)) * ref.linear(x, wu)
     assert_close_bf16(got, want)
 
@@ -211,6 +269,13 @@ def test_action_out_euler(ops):
     want = x + (-0.1) * v
     assert rel_err(xd, want) < 1e-3
     torch.testing.assert_close(xb.cpu(), xd.cpu().to(BF16))
+    # with the final expert RMSNorm fused into the A operand
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16)
+    xd = x.cuda().clone()
+    ops.action_out_euler(a.cuda(), ops.pack_weight(w.cuda()), xd, -0.1,
+                         norm=(nw.cuda(), 1e-5))
+    v = ref.linear(ref.rms_norm(a, nw, 1e-5), w).float()
+    assert rel_err(xd, x + (-0.1) * v) < 1e-3
 
 
 # -------------------------------------------------------------- attention ---

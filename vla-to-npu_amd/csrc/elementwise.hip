@@ -164,15 +164,16 @@ __global__ void transpose_kernel(const bf16* __restrict__ w, long ldw, bf16* __r
   }
 }
 
-// packed row p: block b = p / 16; even blocks are gate rows, odd blocks up rows
+// packed row p: block b = p / 32; even blocks are gate rows, odd blocks up rows
+// (gate column j and up column j are always 32 packed rows apart)
 __global__ void pack_gate_up_kernel(const bf16* __restrict__ wg, const bf16* __restrict__ wu,
                                     bf16* __restrict__ o, int K, int inter) {
   const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= 2L * inter * K) return;
   const int k = idx % K;
   const int prow = idx / K;
-  const int blk = prow >> 4, within = prow & 15;
-  const int j = (blk >> 1) * 16 + within;
+  const int blk = prow >> 5, within = prow & 31;
+  const int j = (blk >> 1) * 32 + within;
   const bf16* src = (blk & 1) ? wu : wg;
   o[idx] = src[(long)k * inter + j];
 }
@@ -300,7 +301,7 @@ int svla_pack_weight_bf16(const void* w_kn, int ldw, void* out_nk, int k, int n,
 
 int svla_pack_gate_up_bf16(const void* w_gate, const void* w_up, void* out, int k, int inter,
                            svla_stream_t stream) {
-  if (k <= 0 || inter <= 0 || inter % 16) return SVLA_EINVAL;
+  if (k <= 0 || inter <= 0 || inter % 32) return SVLA_EINVAL;
   const long n = 2L * inter * k;
   hipLaunchKernelGGL(pack_gate_up_kernel, dim3((n + 255) / 256), dim3(256), 0,
                      (hipStream_t)stream, static_cast<const bf16*>(w_gate),

@@ -1,34 +1,48 @@
-// bf16 MFMA GEMM for gfx950 with fused epilogues.
+// bf16 MFMA GEMM for gfx950 with fused prologues and epilogues.
 //
-//   C[M, N] = epilogue(alpha * A[M, K] . W[N, K]^T)
+//   C[M, N] = epilogue(alpha * norm(A)[M, K] . W[N, K]^T)
 //
 // Replaces the Allo GEMM region (cc/gemm.py:44-77, instantiated e.g. at
-// vla/text_encoder_bf16.py:174-225) and the host-side K-chunk accumulation
-// loops (vla/text_encoder_bf16.py:584-590, vla/connector_bf16.py:116-126).
+// vla/text_encoder_bf16.py:174-225), the host-side K-chunk accumulation
+// loops (vla/text_encoder_bf16.py:584-590, vla/connector_bf16.py:116-126),
+// the RMSNorm in front of every projection (vla/text_encoder_bf16.py:398-404)
+// and the elementwise kernels behind them (RoPE, SiLU*up, GELU, residual add).
 //
 // Design (CDNA4):
-//  * 256 threads = 4 wave64s per workgroup; block tile BM x BN, K step 64.
+//  * 256 threads = 4 wave64s per workgroup, block tile BM x BN, K step 64.
+//    Large problems use 256x256 tiles (each wave 128x128 with
+//    v_mfma_f32_32x32x16_bf16: 64 FLOP per LDS byte) at one workgroup per CU;
+//    mid-size problems 128x128 / 64x128 / 64x64 tiles.
+//  * Skinny-M problems (the bs=1 prefix and expert: M = 50 .. 241 rows) use a
+//    separate kernel: 64-row tiles whose K loop is split over the 4 waves of
+//    the workgroup, MFMA operand fragments loaded straight from global memory
+//    (A and W are both K-contiguous, so a fragment is one 16-byte load per
+//    lane), the 4 partial tiles summed through LDS.  This gives split-K
+//    parallelism without any cross-workgroup reduction, workspace or atomics.
 //  * Global -> register prefetch of the next K tile while the current one is
 //    consumed from LDS; LDS double buffer, one barrier per K step.  LDS rows are
-//    padded by 16 bytes so the 16-byte MFMA operand reads of 8 consecutive rows
-//    hit 8 distinct 4-bank groups.
-//  * v_mfma_f32_16x16x32_bf16 with the WEIGHT tile as the A operand and the
-//    activation tile as the B operand, so each lane's accumulator holds 4
-//    consecutive output COLUMNS of one row: epilogues (bias, RoPE pairs
-//    (d, d+32), SiLU(gate)*up pairs, residual) are lane-local and stores are
+//    padded by 16 bytes so the 16-byte operand reads of 8 consecutive rows hit
+//    distinct bank groups.
+//  * The WEIGHT tile is the MFMA A operand and the activation tile the B
+//    operand, so every lane's accumulator holds runs of 4 consecutive output
+//    COLUMNS of one row: the epilogues (bias, RoPE pairs (d, d+32), SiLU(gate)
+//    * up pairs (gate/up interleaved in blocks of 32 rows, so the partner is
+//    always 32 packed columns away), residual) are lane-local, and stores are
 //    8-byte vectors.
-//  * The A operand can be gathered: the pixel-shuffle of the connector and the
-//    im2col of the patch embedding are folded into the A-tile addressing, so
-//    neither is ever materialised in HBM.
-//  * Small-M shapes (bs=1 prefix / expert) use split-K over an fp32 workspace
-//    plus a reduce kernel that applies the same epilogue (deterministic, no
-//    atomics, no memset -> safe under HIP graph capture).
+//  * A-operand gathers: the pixel-shuffle of the connector and the im2col of
+//    the patch embedding are folded into the A-tile addressing; optionally the
+//    A rows are RMS-normalised on the fly (per-row statistics computed in a
+//    prologue, the tile scaled when it is written to LDS), which removes every
+//    standalone RMSNorm launch of the decoder / expert layers.
+//  * Workgroup ids are remapped so consecutive tiles land on the same XCD
+//    (the hardware deals workgroups round-robin over the 8 XCDs, each with its
+//    own L2): neighbouring tiles share A rows in that XCD's L2.
 #include "svla_common.h"
 
 namespace {
 
 enum AMode { A_DENSE = 0, A_PSHUF = 1, A_PATCH = 2 };
-enum Epi { EPI_STORE = 0, EPI_ROPE = 1, EPI_SILU = 2, EPI_EULER = 3, EPI_PARTIAL = 4 };
+enum Epi { EPI_STORE = 0, EPI_ROPE = 1, EPI_SILU = 2, EPI_EULER = 3 };
 
 struct GemmArgs {
   const bf16* a;
@@ -49,7 +63,6 @@ struct GemmArgs {
   long ldr;
   const bf16* rowadd;  // added after rounding: rowadd[(m % rowadd_period) * N + n]
   int rowadd_period;
-  int act;
   int out_f32;
   const float* rope_cos;
   const float* rope_sin;
@@ -65,11 +78,9 @@ struct GemmArgs {
   // tokens straight into its slot of the [B, prefix_len, H] prefix buffer.
   int c_rpg;
   long c_gstride;
-  // split-K
-  float* ws;
-  long ws_bytes;
-  int splits;
-  int kt_per_split;
+  // fused RMSNorm of the A rows: a = bf16(x * rsqrt(mean(x^2) + eps) * w[k])
+  const bf16* norm_w;
+  float norm_eps;
 };
 
 __device__ __forceinline__ long crow(const GemmArgs& p, int m) {
@@ -78,13 +89,12 @@ __device__ __forceinline__ long crow(const GemmArgs& p, int m) {
   return (long)g * p.c_gstride + (m - g * p.c_rpg);
 }
 
-__device__ __forceinline__ float apply_act(int act, float v) {
-  switch (act) {
-    case SVLA_ACT_GELU_TANH: return gelu_tanh_f(v);
-    case SVLA_ACT_GELU_ERF: return gelu_erf_f(v);
-    case SVLA_ACT_SILU: return silu_f(v);
-    default: return v;
-  }
+template <int ACT>
+__device__ __forceinline__ float apply_act(float v) {
+  if constexpr (ACT == SVLA_ACT_GELU_TANH) return gelu_tanh_f(v);
+  else if constexpr (ACT == SVLA_ACT_GELU_ERF) return gelu_erf_f(v);
+  else if constexpr (ACT == SVLA_ACT_SILU) return silu_f(v);
+  else return v;
 }
 
 __device__ __forceinline__ void store_bf16x4(bf16* dst, const float v[4]) {
@@ -98,8 +108,8 @@ __device__ __forceinline__ void load_bf16x4(const bf16* src, float v[4]) {
   v[0] = bf2f(t[0]); v[1] = bf2f(t[1]); v[2] = bf2f(t[2]); v[3] = bf2f(t[3]);
 }
 
-// ---- epilogues: each handles 4 consecutive columns of one row -------------
-// v already includes alpha.  ACT is a compile-time activation (SVLA_ACT_*).
+// ---- epilogues: 4 consecutive (packed) columns of one row ------------------
+// Values already include alpha.
 template <int ACT>
 __device__ __forceinline__ void epi_store(const GemmArgs& p, int m, int n, float v[4]) {
   if (p.bias) {
@@ -121,7 +131,7 @@ __device__ __forceinline__ void epi_store(const GemmArgs& p, int m, int n, float
   for (int i = 0; i < 4; ++i) v[i] = rbf(v[i]);
   if constexpr (ACT != SVLA_ACT_NONE) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = rbf(apply_act(ACT, v[i]));
+    for (int i = 0; i < 4; ++i) v[i] = rbf(apply_act<ACT>(v[i]));
   }
   if (p.rowadd) {
     float r[4];
@@ -166,13 +176,16 @@ __device__ __forceinline__ void epi_rope(const GemmArgs& p, int m, int n1, float
   }
 }
 
-// gated MLP: out = bf16(bf16(silu(bf16(g))) * bf16(u))  (nn.SiLU on the bf16
-// gate projection, then the bf16 hadamard product, vla/text_encoder_bf16.py:130-131)
-__device__ __forceinline__ void epi_silu(const GemmArgs& p, int m, int nout, float g[4],
+// Gated MLP pair: gate at packed column ng (first half of a 64-block), up at
+// ng + 32; output column (ng / 64) * 32 + ng % 64.
+// out = bf16(bf16(silu(bf16(g))) * bf16(u))  (nn.SiLU on the bf16 gate
+// projection, then the bf16 hadamard product, vla/text_encoder_bf16.py:130-131)
+__device__ __forceinline__ void epi_silu(const GemmArgs& p, int m, int ng, float g[4],
                                          float u[4]) {
   float o[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) o[i] = rbf(silu_f(rbf(g[i]))) * rbf(u[i]);
+  const int nout = (ng >> 6) * 32 + (ng & 63);
   store_bf16x4(reinterpret_cast<bf16*>(p.c) + crow(p, m) * p.ldc + nout, o);
 }
 
@@ -225,54 +238,100 @@ __device__ __forceinline__ bf16x8 load_a(const GemmArgs& p, int m, int k) {
 
 constexpr int BK = 64;
 constexpr int LDS_STRIDE = BK + 8;  // elements; +16 bytes of padding per row
+constexpr int kNumXCD = 8;
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int AMODE, int EPI, int ACT = SVLA_ACT_NONE>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
+// Maps the hardware workgroup id so that consecutive logical tiles (n fastest)
+// share an XCD.
+__device__ __forceinline__ int xcd_remap(int bid, int total) {
+  const int per = total / kNumXCD;
+  const int full = per * kNumXCD;
+  if (bid >= full) return bid;
+  return (bid % kNumXCD) * per + bid / kNumXCD;
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int MF, int AMODE, bool NORM, int EPI,
+          int ACT>
+__global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs p) {
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-  constexpr int TM = WM / 16, TN = WN / 16;
+  constexpr int TM = WM / MF, TN = WN / MF;
+  constexpr int KSTEP = MF == 32 ? 16 : 32;      // K per MFMA
+  constexpr int KFRAG = 8;                        // bf16 per lane per operand
+  constexpr int LG = 64 / MF;                     // lane groups along K
   constexpr int A_CH = BM * BK / 8 / 256;
   constexpr int B_CH = BN * BK / 8 / 256;
+  constexpr int PAIR_T = 32 / MF;                 // tile offset of the +32 column partner
+  using acc_t = typename std::conditional<MF == 32, f32x16, f32x4>::type;
+  constexpr int ACC_N = MF == 32 ? 16 : 4;
   static_assert(WAVES_M * WAVES_N == 4, "4 waves");
   static_assert(A_CH >= 1 && B_CH >= 1, "tile too small");
-  static_assert(EPI != EPI_ROPE || WN % 64 == 0, "RoPE needs whole heads per wave");
-  static_assert(EPI != EPI_SILU || TN % 2 == 0, "SiLU pairs gate/up subtiles");
+  static_assert(LG * KFRAG == KSTEP, "operand layout");
+  static_assert((EPI != EPI_ROPE && EPI != EPI_SILU) || WN % 64 == 0,
+                "paired epilogues need 64-column aligned wave tiles");
+  static_assert(!NORM || AMODE == A_DENSE, "row norm only for dense A");
 
   __shared__ __attribute__((aligned(16))) bf16 sA[2][BM * LDS_STRIDE];
   __shared__ __attribute__((aligned(16))) bf16 sB[2][BN * LDS_STRIDE];
+  __shared__ float s_rs[NORM ? BM : 1];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
-  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int nk_total = (p.K + BK - 1) / BK;
-  int kt_begin = 0, kt_end = nk_total;
-  if constexpr (EPI == EPI_PARTIAL) {
-    kt_begin = blockIdx.z * p.kt_per_split;
-    kt_end = min(nk_total, kt_begin + p.kt_per_split);
+  const int gn = gridDim.x;
+  const int tile = xcd_remap(blockIdx.y * gn + blockIdx.x, gn * gridDim.y);
+  const int tm_idx = tile / gn, tn_idx = tile - (tile / gn) * gn;
+  const int m0 = tm_idx * BM, n0 = tn_idx * BN;
+  const int kt_begin = 0;
+  const int kt_end = (p.K + BK - 1) / BK;
+
+  // ---- prologue: per-row RMS statistics of this block's A rows
+  if constexpr (NORM) {
+    for (int r = wave; r < BM; r += 4) {
+      const int m = m0 + r;
+      float ss = 0.f;
+      if (m < p.M) {
+        const bf16* xr = p.a + (long)m * p.lda;
+        for (int c = lane * 8; c < p.K; c += 512) {
+          const bf16x8 v = ld8(xr + c);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float f = bf2f(v[j]);
+            ss += f * f;
+          }
+        }
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) s_rs[r] = 1.0f / sqrtf(ss / (float)p.K + p.norm_eps);
+    }
+    __syncthreads();
   }
 
-  f32x4 acc[TN][TM];
+  acc_t acc[TN][TM];
 #pragma unroll
   for (int i = 0; i < TN; ++i)
 #pragma unroll
-    for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TM; ++j)
+#pragma unroll
+      for (int e = 0; e < ACC_N; ++e) acc[i][j][e] = 0.f;
 
   bf16x8 ra[A_CH], rb[B_CH];
+  bf16x8 rw;  // norm gain for this thread's A k-chunk (the same for all its chunks)
 
   auto gload = [&](int kt) {
     const int kb = kt * BK;
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int c = tid + i * 256;
-      const int row = c >> 3, kc = c & 7;
-      ra[i] = load_a<AMODE>(p, m0 + row, kb + kc * 8);
+      ra[i] = load_a<AMODE>(p, m0 + (c >> 3), kb + (c & 7) * 8);
+    }
+    if constexpr (NORM) {
+      const int k = kb + (tid & 7) * 8;
+      rw = k < p.K ? ld8(p.norm_w + k) : bf16x8{};
     }
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
       const int c = tid + i * 256;
-      const int row = c >> 3, kc = c & 7;
-      const int n = n0 + row, k = kb + kc * 8;
+      const int n = n0 + (c >> 3), k = kb + (c & 7) * 8;
       rb[i] = (n < p.N && k < p.K) ? ld8(p.b + (long)n * p.ldb + k) : bf16x8{};
     }
   };
@@ -280,7 +339,15 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int c = tid + i * 256;
-      *reinterpret_cast<bf16x8*>(&sA[buf][(c >> 3) * LDS_STRIDE + (c & 7) * 8]) = ra[i];
+      bf16x8 v = ra[i];
+      if constexpr (NORM) {
+        // torch 2.10 nn.RMSNorm on bf16: fp32 x * rsqrt(.) * w, one rounding
+        const float rs = s_rs[c >> 3];
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          v[j] = f2bf(__fmul_rn(__fmul_rn(bf2f(v[j]), rs), bf2f(rw[j])));
+      }
+      *reinterpret_cast<bf16x8*>(&sA[buf][(c >> 3) * LDS_STRIDE + (c & 7) * 8]) = v;
     }
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
@@ -289,8 +356,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
     }
   };
 
-  const int frag_row = lane & 15;
-  const int frag_k = (lane >> 4) * 8;
+  const int frag_row = lane % MF;
+  const int frag_k = (lane / MF) * KFRAG;
 
   if (kt_begin < kt_end) {
     gload(kt_begin);
@@ -300,250 +367,365 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs p) {
       const int cur = (kt - kt_begin) & 1;
       if (kt + 1 < kt_end) gload(kt + 1);
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
+      for (int ks = 0; ks < BK / KSTEP; ++ks) {
         bf16x8 fw[TN], fx[TM];
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn)
           fw[tn] = *reinterpret_cast<const bf16x8*>(
-              &sB[cur][(wn * WN + tn * 16 + frag_row) * LDS_STRIDE + ks * 32 + frag_k]);
+              &sB[cur][(wn * WN + tn * MF + frag_row) * LDS_STRIDE + ks * KSTEP + frag_k]);
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
           fx[tm] = *reinterpret_cast<const bf16x8*>(
-              &sA[cur][(wm * WM + tm * 16 + frag_row) * LDS_STRIDE + ks * 32 + frag_k]);
+              &sA[cur][(wm * WM + tm * MF + frag_row) * LDS_STRIDE + ks * KSTEP + frag_k]);
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-          for (int tm = 0; tm < TM; ++tm)
-            acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[tn], fx[tm], acc[tn][tm],
-                                                                  0, 0, 0);
+          for (int tm = 0; tm < TM; ++tm) {
+            if constexpr (MF == 32)
+              acc[tn][tm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[tn], fx[tm], acc[tn][tm],
+                                                                    0, 0, 0);
+            else
+              acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[tn], fx[tm], acc[tn][tm],
+                                                                    0, 0, 0);
+          }
       }
       if (kt + 1 < kt_end) sstore(cur ^ 1);
       __syncthreads();
     }
   }
 
-  // ---- epilogue: acc[tn][tm][i] = C[m][n], m = row base + (lane & 15),
-  //      n = col base + 4*(lane >> 4) + i
-  const int col_in = 4 * (lane >> 4);
+  // ---- accumulator layout: acc[tn][tm][r] = C[m][n] with
+  //   m = m0 + wm*WM + tm*MF + lane % MF
+  //   n = n0 + wn*WN + tn*MF + run(r) + 4*(lane / MF) + r % 4
+  //   run(r) = 8*(r/4) for MF = 32 (4 runs of 4 columns), 0 for MF = 16.
+  constexpr int RUNS = ACC_N / 4;
+  constexpr int RUN_STRIDE = MF == 32 ? 8 : 0;
+  const int col_in = 4 * (lane / MF);
+
+  // ---- epilogue
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) {
-    const int m = m0 + wm * WM + tm * 16 + (lane & 15);
+    const int m = m0 + wm * WM + tm * MF + (lane % MF);
     if (m >= p.M) continue;
-    if constexpr (EPI == EPI_PARTIAL) {
-      float* w = p.ws + ((long)blockIdx.z * p.M + m) * p.N;
 #pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const int n = n0 + wn * WN + tn * 16 + col_in;
-        if (n < p.N) {
-          const f32x4 a = acc[tn][tm];
-          *reinterpret_cast<f32x4*>(w + n) =
-              f32x4{a[0] * p.alpha, a[1] * p.alpha, a[2] * p.alpha, a[3] * p.alpha};
-        }
-      }
-    } else if constexpr (EPI == EPI_ROPE) {
+    for (int tn = 0; tn < TN; ++tn) {
 #pragma unroll
-      for (int tb = 0; tb < TN; tb += 4) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int n1 = n0 + wn * WN + (tb + h) * 16 + col_in;
-          if (n1 < p.N) {
-            float x1[4], x2[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              x1[i] = acc[tb + h][tm][i] * p.alpha;
-              x2[i] = acc[tb + h + 2][tm][i] * p.alpha;
-            }
-            epi_rope(p, m, n1, x1, x2);
-          }
-        }
-      }
-    } else if constexpr (EPI == EPI_SILU) {
-#pragma unroll
-      for (int tn = 0; tn < TN; tn += 2) {
-        const int ng = n0 + wn * WN + tn * 16;  // gate block start (multiple of 32)
-        if (ng < p.N) {
-          float g[4], u[4];
+      for (int q = 0; q < RUNS; ++q) {
+        const int n = n0 + wn * WN + tn * MF + q * RUN_STRIDE + col_in;
+        if constexpr (EPI == EPI_ROPE || EPI == EPI_SILU) {
+          // first half of each 64-column block pairs with the tile 32 columns on
+          if (((tn * MF) & 63) >= 32 || n >= p.N) continue;
+          float x1[4], x2[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            g[i] = acc[tn][tm][i] * p.alpha;
-            u[i] = acc[tn + 1][tm][i] * p.alpha;
+            x1[i] = acc[tn][tm][4 * q + i] * p.alpha;
+            x2[i] = acc[tn + PAIR_T][tm][4 * q + i] * p.alpha;
           }
-          epi_silu(p, m, ng / 2 + col_in, g, u);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const int n = n0 + wn * WN + tn * 16 + col_in;
-        if (n < p.N) {
+          if constexpr (EPI == EPI_ROPE) epi_rope(p, m, n, x1, x2);
+          else epi_silu(p, m, n, x1, x2);
+        } else {
+          if (n >= p.N) continue;
           float v[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][i] * p.alpha;
-          if constexpr (EPI == EPI_EULER)
-            epi_euler(p, m, n, v);
-          else
-            epi_store<ACT>(p, m, n, v);
+          for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][4 * q + i] * p.alpha;
+          if constexpr (EPI == EPI_EULER) epi_euler(p, m, n, v);
+          else epi_store<ACT>(p, m, n, v);
         }
       }
     }
   }
 }
 
-// Split-K reduction + epilogue.  One thread per epilogue unit.
-template <int EPI, int ACT = SVLA_ACT_NONE>
-__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmArgs p) {
-  const long unit = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long MN = (long)p.M * p.N;
-  auto sum4 = [&](int m, int n, float v[4]) {
-    v[0] = v[1] = v[2] = v[3] = 0.f;
-    for (int s = 0; s < p.splits; ++s) {
-      const f32x4 t = *reinterpret_cast<const f32x4*>(p.ws + s * MN + (long)m * p.N + n);
-      v[0] += t[0]; v[1] += t[1]; v[2] += t[2]; v[3] += t[3];
+// ---- skinny-M GEMM ----------------------------------------------------------
+// One workgroup = 64 rows x BN columns, 8 waves.  The waves split the K loop
+// (in steps of 32) and each accumulates the whole tile with 16x16x32 MFMAs
+// whose operand fragments come straight from global memory.  Problems this
+// small are latency-bound, so each wave issues the loads of up to KR k-steps
+// at once before any MFMA, and the optional RMS statistics of the A rows are
+// gathered while those loads are in flight.  The 8 partial tiles are summed
+// through LDS and all 512 threads run the epilogue.
+constexpr int SK_WAVES = 8;
+
+// 16-byte load that is always issued (address clamped into the tensor) and
+// zeroed when out of range: no divergent branch around the load.
+__device__ __forceinline__ bf16x8 ld8_or_zero(const bf16* base, long off, long off_clamped,
+                                              bool valid) {
+  const bf16x8 v = ld8(base + (valid ? off : off_clamped));
+  return valid ? v : bf16x8{};
+}
+
+template <int BN, int AMODE, bool NORM, int EPI, int ACT>
+__global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
+  constexpr int BM = 64, TM = BM / 16, TN = BN / 16;
+  constexpr int PS = BN + 4;  // padded LDS row of a partial tile (floats)
+  constexpr int NT = SK_WAVES * 64;
+  // k-steps whose loads are in flight together (bounded by the 256-VGPR budget
+  // of 8 waves per workgroup)
+  constexpr int KR = NORM ? (BN == 32 ? 4 : 2) : (BN == 32 && AMODE == A_DENSE ? 8 : 4);
+  static_assert((EPI != EPI_ROPE && EPI != EPI_SILU) || BN % 64 == 0, "paired epilogue");
+  static_assert(!NORM || AMODE == A_DENSE, "row norm only for dense A");
+  __shared__ __attribute__((aligned(16))) float s_part[SK_WAVES][BM * PS];
+  __shared__ float s_rs[NORM ? BM : 1];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const int nks = (p.K + 31) / 32;
+  const int per = (nks + SK_WAVES - 1) / SK_WAVES;
+  const int ks0 = wave * per, ks1 = min(nks, ks0 + per);
+  const int fr = lane & 15, fk = (lane >> 4) * 8;
+
+  f32x4 acc[TN][TM];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  bf16x8 fw[KR][TN], fx[KR][TM], fg[KR];
+  auto load_round = [&](int base) {
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+      const int ks = base + r;
+      if (ks >= ks1) {  // wave-uniform: no loads for k-steps past this wave's range
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) fw[r][tn] = bf16x8{};
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm) fx[r][tm] = bf16x8{};
+        if constexpr (NORM) fg[r] = bf16x8{};
+        continue;
+      }
+      const int k = ks * 32 + fk;
+      const bool kin = k < p.K;
+      const int kc = min(k, p.K - 8);
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int n = n0 + tn * 16 + fr;
+        const int nc = min(n, p.N - 1);
+        fw[r][tn] = ld8_or_zero(p.b, (long)n * p.ldb + k, (long)nc * p.ldb + kc, kin && n < p.N);
+      }
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+        if constexpr (AMODE == A_DENSE) {
+          const int m = m0 + tm * 16 + fr;
+          const int mc = min(m, p.M - 1);
+          fx[r][tm] = ld8_or_zero(p.a, (long)m * p.lda + k, (long)mc * p.lda + kc, kin && m < p.M);
+        } else {
+          fx[r][tm] = kin ? load_a<AMODE>(p, m0 + tm * 16 + fr, k) : bf16x8{};
+        }
+      }
+      if constexpr (NORM) fg[r] = ld8_or_zero(p.norm_w, k, kc, kin);
     }
   };
-  if constexpr (EPI == EPI_ROPE) {
-    // units: (m, 64-block b, q in 0..7) -> columns b*64 + 4q and +32
-    const int per_row = p.N / 64 * 8;
-    if (unit >= (long)p.M * per_row) return;
-    const int m = unit / per_row, r = unit - (long)m * per_row;
-    const int n1 = (r >> 3) * 64 + (r & 7) * 4;
-    float x1[4], x2[4];
-    sum4(m, n1, x1);
-    sum4(m, n1 + 32, x2);
-    epi_rope(p, m, n1, x1, x2);
-  } else if constexpr (EPI == EPI_SILU) {
-    // units: (m, 32-block b, q in 0..3) -> gate b*32 + 4q, up +16, out b*16 + 4q
-    const int per_row = p.N / 32 * 4;
-    if (unit >= (long)p.M * per_row) return;
-    const int m = unit / per_row, r = unit - (long)m * per_row;
-    const int ng = (r >> 2) * 32 + (r & 3) * 4;
-    float g[4], u[4];
-    sum4(m, ng, g);
-    sum4(m, ng + 16, u);
-    epi_silu(p, m, (r >> 2) * 16 + (r & 3) * 4, g, u);
+  float rs[TM];
+  auto mma_round = [&](int base) {
+#pragma unroll
+    for (int r = 0; r < KR; ++r) {
+      if (base + r >= ks1) break;  // wave-uniform
+      if constexpr (NORM) {
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+          for (int j = 0; j < 8; ++j)
+            fx[r][tm][j] =
+                f2bf(__fmul_rn(__fmul_rn(bf2f(fx[r][tm][j]), rs[tm]), bf2f(fg[r][j])));
+      }
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+          acc[tn][tm] =
+              __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[r][tn], fx[r][tm], acc[tn][tm], 0, 0, 0);
+    }
+  };
+
+  load_round(ks0);
+  if constexpr (NORM) {
+    // row statistics while the first round of operand loads is in flight:
+    // thread (row = tid / 8, part = tid % 8) sums chunks part, part + 8, ...
+    // of its row, accumulating as the loads land; 8 lanes then combine.
+    const int row = tid >> 3, part = tid & 7;
+    const int m = m0 + row;
+    const int mc = min(m, p.M - 1);
+    const bf16* xr = p.a + (long)mc * p.lda;
+    float ss = 0.f;
+#pragma unroll 4
+    for (int c = part * 8; c < p.K; c += 64) {
+      const bf16x8 v = ld8(xr + c);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float f = bf2f(v[e]);
+        ss += f * f;
+      }
+    }
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    ss += __shfl_xor(ss, 4, 64);
+    if (part == 0) s_rs[row] = 1.0f / sqrtf(ss / (float)p.K + p.norm_eps);
+    __syncthreads();
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) rs[tm] = s_rs[tm * 16 + fr];
+  }
+  mma_round(ks0);
+  for (int base = ks0 + KR; base < ks1; base += KR) {
+    load_round(base);
+    mma_round(base);
+  }
+
+  // partial tile: element (m_l, n_l) at s_part[wave][m_l * PS + n_l]
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+      *reinterpret_cast<f32x4*>(&s_part[wave][(tm * 16 + fr) * PS + tn * 16 + 4 * (lane >> 4)]) =
+          acc[tn][tm];
+  __syncthreads();
+
+  auto sum4 = [&](int ml, int nl, float v[4]) {
+    f32x4 t = *reinterpret_cast<const f32x4*>(&s_part[0][ml * PS + nl]);
+#pragma unroll
+    for (int w = 1; w < SK_WAVES; ++w)
+      t += *reinterpret_cast<const f32x4*>(&s_part[w][ml * PS + nl]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = t[i] * p.alpha;
+  };
+  if constexpr (EPI == EPI_ROPE || EPI == EPI_SILU) {
+    constexpr int UPR = BN / 64 * 8;  // units per row: (64-block, 4-column group of the first half)
+    for (int u = tid; u < BM * UPR; u += NT) {
+      const int ml = u / UPR, r = u - ml * UPR;
+      const int nl = (r >> 3) * 64 + (r & 7) * 4;
+      const int m = m0 + ml, n = n0 + nl;
+      if (m >= p.M || n >= p.N) continue;
+      float x1[4], x2[4];
+      sum4(ml, nl, x1);
+      sum4(ml, nl + 32, x2);
+      if constexpr (EPI == EPI_ROPE) epi_rope(p, m, n, x1, x2);
+      else epi_silu(p, m, n, x1, x2);
+    }
   } else {
-    const int per_row = p.N / 4;
-    if (unit >= (long)p.M * per_row) return;
-    const int m = unit / per_row, n = (unit - (long)m * per_row) * 4;
-    float v[4];
-    sum4(m, n, v);
-    epi_store<ACT>(p, m, n, v);
+    constexpr int UPR = BN / 4;
+    for (int u = tid; u < BM * UPR; u += NT) {
+      const int ml = u / UPR, nl = (u - ml * UPR) * 4;
+      const int m = m0 + ml, n = n0 + nl;
+      if (m >= p.M || n >= p.N) continue;
+      float v[4];
+      sum4(ml, nl, v);
+      if constexpr (EPI == EPI_EULER) epi_euler(p, m, n, v);
+      else epi_store<ACT>(p, m, n, v);
+    }
   }
 }
 
 // ---- launch ---------------------------------------------------------------
-struct TileCfg {
-  int bm, bn;
-};
+enum TileId { T256 = 0, T128 = 1, T64x128 = 2, T64 = 3, S64 = 4, S32 = 5, T128S = 6,
+              NUM_TILES = 7 };
 
-template <int AMODE, int EPI, int ACT = SVLA_ACT_NONE>
-int launch_cfg(const TileCfg& t, dim3 grid, GemmArgs& p, hipStream_t s) {
-  if (t.bm == 128)
-    hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, AMODE, EPI, ACT>), grid, dim3(256), 0, s, p);
-  else if (t.bm == 64 && t.bn == 128)
-    hipLaunchKernelGGL((gemm_kernel<64, 128, 2, 2, AMODE, EPI, ACT>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((gemm_kernel<64, 64, 4, 1, AMODE, EPI, ACT>), grid, dim3(256), 0, s, p);
-  SVLA_CHECK_LAUNCH();
-  return 0;
-}
-
-template <int EPI>
-void launch_reduce(int act, int blocks, GemmArgs& p, hipStream_t s) {
-  switch (act) {
-    case SVLA_ACT_GELU_TANH:
-      hipLaunchKernelGGL((splitk_reduce_kernel<EPI, SVLA_ACT_GELU_TANH>), dim3(blocks), dim3(256), 0, s, p);
+template <int AMODE, bool NORM, int EPI, int ACT>
+void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
+  switch (t) {
+    case T256:
+      hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 2, 32, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
       break;
-    case SVLA_ACT_GELU_ERF:
-      hipLaunchKernelGGL((splitk_reduce_kernel<EPI, SVLA_ACT_GELU_ERF>), dim3(blocks), dim3(256), 0, s, p);
+    case T128:
+      hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 32, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
       break;
-    case SVLA_ACT_SILU:
-      hipLaunchKernelGGL((splitk_reduce_kernel<EPI, SVLA_ACT_SILU>), dim3(blocks), dim3(256), 0, s, p);
+    case T64x128:
+      hipLaunchKernelGGL((gemm_kernel<64, 128, 2, 2, 16, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      break;
+    case T64:
+      hipLaunchKernelGGL((gemm_kernel<64, 64, 4, 1, 16, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      break;
+    case T128S:
+      hipLaunchKernelGGL((gemm_kernel<128, 128, 2, 2, 16, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      break;
+    case S64:
+      hipLaunchKernelGGL((skinny_kernel<64, AMODE, NORM, EPI, ACT>), grid, dim3(SK_WAVES * 64), 0, s, p);
       break;
     default:
-      hipLaunchKernelGGL((splitk_reduce_kernel<EPI, SVLA_ACT_NONE>), dim3(blocks), dim3(256), 0, s, p);
+      if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
+        hipLaunchKernelGGL((skinny_kernel<32, AMODE, NORM, EPI, ACT>), grid, dim3(SK_WAVES * 64), 0, s, p);
   }
 }
 
 constexpr int kNumCU = 256;
+constexpr int kSkinnyMaxM = 256;
 
-TileCfg pick_tile(int M, int N) {
+struct TileCfg {
+  TileId id;
+  int bm, bn;
+};
+
+// Tuning override (svla_gemm_set_tile): -1 = automatic choice.
+int g_force_tile = -1;
+
+TileCfg tile_dims(TileId id) {
+  switch (id) {
+    case T256: return {T256, 256, 256};
+    case T128: return {T128, 128, 128};
+    case T128S: return {T128S, 128, 128};
+    case T64x128: return {T64x128, 64, 128};
+    case T64: return {T64, 64, 64};
+    case S64: return {S64, 64, 64};
+    default: return {S32, 64, 32};
+  }
+}
+
+TileCfg pick_tile(int M, int N, int epi) {
   auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  if (M >= 512 && tiles(128, 128) >= kNumCU) return {128, 128};
-  if (M >= 128 && tiles(64, 128) >= kNumCU / 2) return {64, 128};
-  return {64, 64};
+  const bool paired_ = epi == EPI_ROPE || epi == EPI_SILU;
+  if (g_force_tile >= 0 && !(paired_ && g_force_tile == S32)) return tile_dims((TileId)g_force_tile);
+  const bool paired = epi == EPI_ROPE || epi == EPI_SILU;
+  if (M <= kSkinnyMaxM) {
+    if (!paired && tiles(64, 64) < kNumCU / 2) return {S32, 64, 32};
+    return {S64, 64, 64};
+  }
+  // measured on MI355X: 128x128 tiles win once the grid has ~4 waves of
+  // workgroups; below that the 64x64 tile's larger grid wins
+  if (M >= 4096 || tiles(128, 128) >= 4 * kNumCU) return {T128, 128, 128};
+  return {T64, 64, 64};
+}
+
+template <int AMODE, bool NORM>
+int dispatch(const GemmArgs& p, int epi, int act, TileId t, dim3 grid, hipStream_t s) {
+  switch (epi) {
+    case EPI_ROPE: launch_tile<AMODE, NORM, EPI_ROPE, 0>(t, grid, p, s); break;
+    case EPI_SILU: launch_tile<AMODE, NORM, EPI_SILU, 0>(t, grid, p, s); break;
+    case EPI_EULER: launch_tile<AMODE, NORM, EPI_EULER, 0>(t, grid, p, s); break;
+    default:
+      switch (act) {
+        case SVLA_ACT_GELU_TANH: launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_GELU_TANH>(t, grid, p, s); break;
+        case SVLA_ACT_GELU_ERF: launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_GELU_ERF>(t, grid, p, s); break;
+        case SVLA_ACT_SILU: launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_SILU>(t, grid, p, s); break;
+        default: launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_NONE>(t, grid, p, s);
+      }
+  }
+  SVLA_CHECK_LAUNCH();
+  return 0;
 }
 
 template <int AMODE>
-int run_gemm(GemmArgs& p, int epi, hipStream_t s) {
-  if (p.M <= 0 || p.N <= 0 || p.K <= 0) return p.M == 0 ? 0 : SVLA_EINVAL;
+int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
+  if (p.M < 0 || p.N <= 0 || p.K <= 0) return SVLA_EINVAL;
+  if (p.M == 0) return 0;
   if (p.K % 8 || p.N % 4 || p.ldb % 8 || p.ldc % 4) return SVLA_EINVAL;
   if (AMODE == A_DENSE && (p.lda % 8 || !svla_aligned16(p.a))) return SVLA_EINVAL;
   if (!svla_aligned16(p.b) || !svla_aligned16(p.c)) return SVLA_EINVAL;
   if (p.res && (p.ldr % 4)) return SVLA_EINVAL;
-  if (epi == EPI_ROPE && (p.N % 64 || p.rope_cols % 64 || p.rope_period <= 0)) return SVLA_EINVAL;
-  if (epi == EPI_SILU && p.N % 32) return SVLA_EINVAL;
-  if (AMODE != A_DENSE && p.act) return SVLA_EINVAL;
+  if ((epi == EPI_ROPE || epi == EPI_SILU) && p.N % 64) return SVLA_EINVAL;
+  if (epi == EPI_ROPE && (p.rope_cols % 64 || p.rope_period <= 0)) return SVLA_EINVAL;
+  if (AMODE != A_DENSE && act) return SVLA_EINVAL;
+  if (p.norm_w && (AMODE != A_DENSE || !svla_aligned16(p.norm_w))) return SVLA_EINVAL;
 
-  TileCfg t = pick_tile(p.M, p.N);
+  const TileCfg t = pick_tile(p.M, p.N, epi);
+  if (p.norm_w && p.K > 2048) return SVLA_EINVAL;  // row statistics keep <= 2048 per row
   const int gm = (p.M + t.bm - 1) / t.bm, gn = (p.N + t.bn - 1) / t.bn;
-  const int nk = (p.K + BK - 1) / BK;
-  // split-K when the tile grid leaves most CUs idle and the K loop is long;
-  // the fp32 partials [splits, M, N] must fit the caller's workspace
-  int splits = 1;
-  const long tiles = (long)gm * gn;
-  if (epi != EPI_EULER && p.ws && tiles < kNumCU && nk >= 8) {
-    int want = (int)((2 * kNumCU + tiles - 1) / tiles);
-    want = min(want, nk / 4);
-    want = min(want, 16);
-    const long per_split = (long)p.M * p.N * 4;
-    while (want > 1 && want * per_split > p.ws_bytes) --want;
-    splits = max(1, want);
-  }
-  if (splits > 1) {
-    const int per = (nk + splits - 1) / splits;
-    splits = (nk + per - 1) / per;
-    p.splits = splits;
-    p.kt_per_split = per;
-    dim3 grid(gn, gm, splits);
-    int rc = launch_cfg<AMODE, EPI_PARTIAL>(t, grid, p, s);
-    if (rc) return rc;
-    long units;
-    if (epi == EPI_ROPE) units = (long)p.M * (p.N / 64) * 8;
-    else if (epi == EPI_SILU) units = (long)p.M * (p.N / 32) * 4;
-    else units = (long)p.M * (p.N / 4);
-    const int blocks = (int)((units + 255) / 256);
-    if (epi == EPI_ROPE)
-      hipLaunchKernelGGL(splitk_reduce_kernel<EPI_ROPE>, dim3(blocks), dim3(256), 0, s, p);
-    else if (epi == EPI_SILU)
-      hipLaunchKernelGGL(splitk_reduce_kernel<EPI_SILU>, dim3(blocks), dim3(256), 0, s, p);
-    else
-      launch_reduce<EPI_STORE>(p.act, blocks, p, s);
-    SVLA_CHECK_LAUNCH();
-    return 0;
-  }
   dim3 grid(gn, gm, 1);
   if constexpr (AMODE == A_DENSE) {
-    switch (epi) {
-      case EPI_ROPE: return launch_cfg<AMODE, EPI_ROPE>(t, grid, p, s);
-      case EPI_SILU: return launch_cfg<AMODE, EPI_SILU>(t, grid, p, s);
-      case EPI_EULER: return launch_cfg<AMODE, EPI_EULER>(t, grid, p, s);
-      default:
-        switch (p.act) {
-          case SVLA_ACT_GELU_TANH: return launch_cfg<AMODE, EPI_STORE, SVLA_ACT_GELU_TANH>(t, grid, p, s);
-          case SVLA_ACT_GELU_ERF: return launch_cfg<AMODE, EPI_STORE, SVLA_ACT_GELU_ERF>(t, grid, p, s);
-          case SVLA_ACT_SILU: return launch_cfg<AMODE, EPI_STORE, SVLA_ACT_SILU>(t, grid, p, s);
-          default: return launch_cfg<AMODE, EPI_STORE>(t, grid, p, s);
-        }
-    }
-  } else {
-    if (epi != EPI_STORE) return SVLA_EINVAL;
-    return launch_cfg<AMODE, EPI_STORE>(t, grid, p, s);
+    if (p.norm_w) return dispatch<AMODE, true>(p, epi, act, t.id, grid, s);
   }
+  return dispatch<AMODE, false>(p, epi, act, t.id, grid, s);
 }
 
 GemmArgs base_args(const void* a, long lda, const void* w, long ldw, void* c, long ldc, int m,
-                   int n, int k, float* ws, long ws_bytes) {
+                   int n, int k) {
   GemmArgs p{};
   p.a = static_cast<const bf16*>(a);
   p.lda = lda;
@@ -555,8 +737,6 @@ GemmArgs base_args(const void* a, long lda, const void* w, long ldw, void* c, lo
   p.N = n;
   p.K = k;
   p.alpha = 1.0f;
-  p.ws = ws;
-  p.ws_bytes = ws ? ws_bytes : 0;
   return p;
 }
 
@@ -564,91 +744,105 @@ GemmArgs base_args(const void* a, long lda, const void* w, long ldw, void* c, lo
 
 extern "C" {
 
-int svla_version(void) { return 100; }
+int svla_version(void) { return 200; }
+
+int svla_gemm_set_tile(int tile) {
+  if (tile < -1 || tile >= NUM_TILES) return SVLA_EINVAL;
+  g_force_tile = tile;
+  return SVLA_OK;
+}
 
 int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
                      const float* bias_f32, const void* res, int ldr, void* c, int ldc, int m,
-                     int n, int k, float alpha, int act, int out_f32, float* ws, long ws_bytes,
-                     svla_stream_t stream) {
+                     int n, int k, float alpha, int act, int out_f32, const void* norm_w,
+                     float norm_eps, svla_stream_t stream) {
   if (act < 0 || act > SVLA_ACT_SILU) return SVLA_EINVAL;
   if (out_f32 && (act || res)) return SVLA_EINVAL;
-  GemmArgs p = base_args(a, lda, w, ldw, c, ldc, m, n, k, ws, ws_bytes);
+  GemmArgs p = base_args(a, lda, w, ldw, c, ldc, m, n, k);
   p.alpha = alpha;
   p.bias = static_cast<const bf16*>(bias);
   p.bias_f32 = bias_f32;
   p.res = static_cast<const bf16*>(res);
   p.ldr = ldr;
-  p.act = act;
   p.out_f32 = out_f32;
-  return run_gemm<A_DENSE>(p, EPI_STORE, (hipStream_t)stream);
+  p.norm_w = static_cast<const bf16*>(norm_w);
+  p.norm_eps = norm_eps;
+  return run_gemm<A_DENSE>(p, EPI_STORE, act, (hipStream_t)stream);
 }
 
 int svla_linear_rope_bf16(const void* a, int lda, const void* w, int ldw, void* c, int ldc,
                           int m, int n, int k, int rope_cols, int seq_len, const float* cos_t,
-                          const float* sin_t, float* ws, long ws_bytes, svla_stream_t stream) {
+                          const float* sin_t, const void* norm_w, float norm_eps,
+                          svla_stream_t stream) {
   if (!cos_t || !sin_t || rope_cols > n) return SVLA_EINVAL;
-  GemmArgs p = base_args(a, lda, w, ldw, c, ldc, m, n, k, ws, ws_bytes);
+  GemmArgs p = base_args(a, lda, w, ldw, c, ldc, m, n, k);
   p.rope_cos = cos_t;
   p.rope_sin = sin_t;
   p.rope_cols = rope_cols;
   p.rope_period = seq_len;
-  return run_gemm<A_DENSE>(p, EPI_ROPE, (hipStream_t)stream);
+  p.norm_w = static_cast<const bf16*>(norm_w);
+  p.norm_eps = norm_eps;
+  return run_gemm<A_DENSE>(p, EPI_ROPE, 0, (hipStream_t)stream);
 }
 
 int svla_linear_silu_mul_bf16(const void* a, int lda, const void* w_gu, int ldw, void* out,
-                              int ldo, int m, int inter, int k, float* ws, long ws_bytes,
-                              svla_stream_t stream) {
-  if (inter % 16) return SVLA_EINVAL;
-  GemmArgs p = base_args(a, lda, w_gu, ldw, out, ldo, m, 2 * inter, k, ws, ws_bytes);
-  return run_gemm<A_DENSE>(p, EPI_SILU, (hipStream_t)stream);
+                              int ldo, int m, int inter, int k, const void* norm_w,
+                              float norm_eps, svla_stream_t stream) {
+  if (inter % 32) return SVLA_EINVAL;
+  GemmArgs p = base_args(a, lda, w_gu, ldw, out, ldo, m, 2 * inter, k);
+  p.norm_w = static_cast<const bf16*>(norm_w);
+  p.norm_eps = norm_eps;
+  return run_gemm<A_DENSE>(p, EPI_SILU, 0, (hipStream_t)stream);
 }
 
 int svla_patch_embed_bf16(const void* images, const void* w, const void* bias, const void* pos,
                           void* out, int ldo, int n_img, int chans, int image, int patch,
-                          int embed, float* ws, long ws_bytes, svla_stream_t stream) {
+                          int embed, svla_stream_t stream) {
   if (patch % 8 || image % patch || !svla_aligned16(images)) return SVLA_EINVAL;
+  if (pos && !svla_aligned16(pos)) return SVLA_EINVAL;
   const int G = image / patch;
   const int K = chans * patch * patch;
-  GemmArgs p = base_args(images, 0, w, K, out, ldo, n_img * G * G, embed, K, ws, ws_bytes);
+  GemmArgs p = base_args(images, 0, w, K, out, ldo, n_img * G * G, embed, K);
   p.p_chans = chans;
   p.p_img = image;
   p.p_patch = patch;
   p.bias = static_cast<const bf16*>(bias);
   p.rowadd = static_cast<const bf16*>(pos);
   p.rowadd_period = G * G;
-  if (pos && !svla_aligned16(pos)) return SVLA_EINVAL;
-  return run_gemm<A_PATCH>(p, EPI_STORE, (hipStream_t)stream);
+  return run_gemm<A_PATCH>(p, EPI_STORE, 0, (hipStream_t)stream);
 }
 
 int svla_connector_bf16(const void* x, const void* w, int ldw, void* out, int ldo, int n_img,
                         int grid, int hidden, int scale, int n_out, int rows_per_sample,
-                        int sample_stride, float* ws, long ws_bytes, svla_stream_t stream) {
+                        int sample_stride, svla_stream_t stream) {
   if (hidden % 8 || grid % scale || !svla_aligned16(x)) return SVLA_EINVAL;
   if (rows_per_sample < 0 || (rows_per_sample > 0 && sample_stride < rows_per_sample))
     return SVLA_EINVAL;
   const int gs = grid / scale;
   const int K = hidden * scale * scale;
-  GemmArgs p = base_args(x, 0, w, ldw, out, ldo, n_img * gs * gs, n_out, K, ws, ws_bytes);
+  GemmArgs p = base_args(x, 0, w, ldw, out, ldo, n_img * gs * gs, n_out, K);
   p.g_grid = grid;
   p.g_hidden = hidden;
   p.g_scale = scale;
   p.c_rpg = rows_per_sample;
   p.c_gstride = sample_stride;
-  return run_gemm<A_PSHUF>(p, EPI_STORE, (hipStream_t)stream);
+  return run_gemm<A_PSHUF>(p, EPI_STORE, 0, (hipStream_t)stream);
 }
 
 int svla_action_out_euler(const void* a, int lda, const void* w, int ldw, float* x_f32,
-                          int ldx, void* x_bf16, int ldxb, int m, int n, int k, float dt,
-                          svla_stream_t stream) {
+                          int ldx, void* x_bf16, int ldxb, int m, int n, int k,
+                          const void* norm_w, float norm_eps, float dt, svla_stream_t stream) {
   if (!x_f32 || ldx % 4 || (x_bf16 && ldxb % 4)) return SVLA_EINVAL;
   // c is unused by the Euler epilogue but must satisfy the alignment check
-  GemmArgs p = base_args(a, lda, w, ldw, x_f32, 4, m, n, k, nullptr, 0);
+  GemmArgs p = base_args(a, lda, w, ldw, x_f32, 4, m, n, k);
   p.x_f32 = x_f32;
   p.ldx = ldx;
   p.x_bf16 = static_cast<bf16*>(x_bf16);
   p.ldxb = ldxb;
   p.dt = dt;
-  return run_gemm<A_DENSE>(p, EPI_EULER, (hipStream_t)stream);
+  p.norm_w = static_cast<const bf16*>(norm_w);
+  p.norm_eps = norm_eps;
+  return run_gemm<A_DENSE>(p, EPI_EULER, 0, (hipStream_t)stream);
 }
 
 }  // extern "C"

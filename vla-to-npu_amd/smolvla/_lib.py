@@ -23,13 +23,14 @@ SIGNATURES = {
     "svla_version": [],
     "svla_rmsnorm_bf16": [_p, _i, _p, _p, _i, _i, _i, _f, _p],
     "svla_layernorm_bf16": [_p, _i, _p, _p, _p, _i, _i, _i, _f, _p],
-    "svla_linear_bf16": [_p, _i, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _i, _i, _p, _l,
+    "svla_gemm_set_tile": [_i],
+    "svla_linear_bf16": [_p, _i, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _i, _i, _p, _f,
                          _p],
-    "svla_linear_rope_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _l, _p],
-    "svla_linear_silu_mul_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _p, _l, _p],
-    "svla_patch_embed_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p, _l, _p],
-    "svla_connector_bf16": [_p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p, _l, _p],
-    "svla_action_out_euler": [_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _f, _p],
+    "svla_linear_rope_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _f, _p],
+    "svla_linear_silu_mul_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _p, _f, _p],
+    "svla_patch_embed_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
+    "svla_connector_bf16": [_p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p],
+    "svla_action_out_euler": [_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _p, _f, _f, _p],
     "svla_attention_bf16": [_p, _i, _l, _p, _i, _l, _p, _i, _l, _p, _i, _l, _i, _i, _i, _i, _i,
                             _i, _f, _i, _i, _p],
     "svla_masked_softmax_bf16": [_p, _i, _p, _i, _i, _p],
@@ -45,6 +46,8 @@ SIGNATURES = {
     "svla_time_embedding_bf16": [_d, _i, _d, _d, _p, _p],
     "svla_f32_to_bf16": [_p, _p, _l, _p],
 }
+
+RESTYPES = {}
 
 _LIB = None
 
@@ -62,7 +65,7 @@ def load(path: pathlib.Path = LIB_PATH):
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_int
+        fn.restype = RESTYPES.get(name, ctypes.c_int)
     _LIB = lib
     return lib
 

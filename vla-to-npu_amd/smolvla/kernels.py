@@ -99,7 +99,7 @@ def softmax_float32_seq1024(scores, weights):
 def transpose_matmul_with_scale_bf16(A, B, C, scale=0.125):
     """C = scale * A . B^T (cc/bf16_old/transpose_matmul_with_scale_bf16.cc:52).
     ``B`` is already in the packed [N, K] form the GEMM consumes."""
-    ops.linear(A, B, alpha=scale, out=C, ws=False)
+    ops.linear(A, B, alpha=scale, out=C)
 
 
 def gemm(A, B, C):

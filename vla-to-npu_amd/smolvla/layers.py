@@ -5,10 +5,10 @@ Weights are prepared once into the packed layouts the kernels consume
 current stream, writing into caller-provided buffers so a whole chunk can be
 captured in one HIP graph.  Activations are row-major ``[B*S, H]`` bf16.
 
-Per decoder layer (vla/text_encoder_bf16.py:480-595 -> 7 launches):
-  rmsnorm -> QKV GEMM with RoPE epilogue -> fused GQA attention ->
-  O GEMM + residual -> rmsnorm -> gate|up GEMM with SiLU*up epilogue ->
-  down GEMM + residual.
+Per decoder layer (vla/text_encoder_bf16.py:480-595 -> 5 launches):
+  [RMSNorm -> QKV GEMM -> RoPE] -> fused GQA attention -> [O GEMM + residual]
+  -> [RMSNorm -> gate|up GEMM -> SiLU*up] -> [down GEMM + residual]
+(brackets = one kernel: the norms run in the GEMM's A-operand prologue).
 """
 
 from __future__ import annotations
@@ -112,7 +112,7 @@ class Buffers:
 
 # ----------------------------------------------------------------- layers ---
 def decoder_layer(x, P, cfg: DecoderConfig, B, L, rope: Rope, mask="causal", prefix_len=0,
-                  bufs: Optional[Buffers] = None, qkv_out=None, ws=None, mid_out=None):
+                  bufs: Optional[Buffers] = None, qkv_out=None, mid_out=None):
     """One SmolLM2-style block on ``x [B*L, H]`` **in place**; returns the
     fused projection buffer ``[B*L, q|k|v]`` whose K (post-RoPE) and V column
     slices are this layer's KV cache (vla/text_encoder_bf16.py:480-595).
@@ -121,36 +121,36 @@ def decoder_layer(x, P, cfg: DecoderConfig, B, L, rope: Rope, mask="causal", pre
     M = B * L
     qd, kvd = cfg.q_dim, cfg.kv_dim
     eps = resolve_eps(cfg.rms_eps)
-    h = ops.rmsnorm(x, P["n1"], eps, out=bufs.get("h", M, cfg.hidden))
     qkv = qkv_out if qkv_out is not None else bufs.get("qkv", M, qd + 2 * kvd)
-    ops.linear_rope(h, P["wqkv"], qd + kvd, L, rope.cos, rope.sin, out=qkv, ws=ws)
+    ops.linear_rope(x, P["wqkv"], qd + kvd, L, rope.cos, rope.sin, out=qkv,
+                    norm=(P["n1"], eps))
     q3 = qkv.view(B, L, -1)
     attn = bufs.get("attn", M, qd)
     ops.attention(q3[:, :, :qd], q3[:, :, qd:qd + kvd], q3[:, :, qd + kvd:],
                   attn.view(B, L, qd), cfg.n_q_heads, cfg.n_kv_heads, mask, prefix_len)
-    ops.linear(attn, P["wo"], res=x, out=x, ws=ws)
+    ops.linear(attn, P["wo"], res=x, out=x)
     if mid_out is not None:
         mid_out.copy_(x)
-    _mlp(x, P, cfg, M, eps, bufs, ws)
+    _mlp(x, P, cfg, M, eps, bufs)
     return qkv
 
 
-def _mlp(x, P, cfg, M, eps, bufs, ws):
-    h = ops.rmsnorm(x, P["n2"], eps, out=bufs.get("h", M, cfg.hidden))
-    act = ops.linear_silu_mul(h, P["wgu"], out=bufs.get("mlp", M, cfg.inter), ws=ws)
-    ops.linear(act, P["wd"], res=x, out=x, ws=ws)
+def _mlp(x, P, cfg, M, eps, bufs):
+    act = ops.linear_silu_mul(x, P["wgu"], out=bufs.get("mlp", M, cfg.inter),
+                              norm=(P["n2"], eps))
+    ops.linear(act, P["wd"], res=x, out=x)
 
 
-def cross_kv(k_src, v_src, P, out_k=None, out_v=None, ws=None):
+def cross_kv(k_src, v_src, P, out_k=None, out_v=None):
     """Cross-attention K/V projections of the prefix cache
     (vla/action_expert_bf16.py:757-758)."""
-    k = ops.linear(k_src, P["wkc"], out=out_k, ws=ws)
-    v = ops.linear(v_src, P["wvc"], out=out_v, ws=ws)
+    k = ops.linear(k_src, P["wkc"], out=out_k)
+    v = ops.linear(v_src, P["wvc"], out=out_v)
     return k, v
 
 
 def cross_layer(x, ck, cv, P, cfg: DecoderConfig, B, L, Lc, rope: Rope,
-                bufs: Optional[Buffers] = None, ws=None):
+                bufs: Optional[Buffers] = None):
     """Expert cross-attention block on ``x [B*L, H]`` in place, attending to
     the already projected ``ck``/``cv [B*Lc, kv]`` (vla/action_expert_bf16.py:731-803;
     RoPE on Q only, no mask)."""
@@ -158,29 +158,29 @@ def cross_layer(x, ck, cv, P, cfg: DecoderConfig, B, L, Lc, rope: Rope,
     M = B * L
     qd = cfg.q_dim
     eps = resolve_eps(cfg.rms_eps)
-    h = ops.rmsnorm(x, P["n1"], eps, out=bufs.get("h", M, cfg.hidden))
-    q = ops.linear_rope(h, P["wq"], qd, L, rope.cos, rope.sin, out=bufs.get("q", M, qd), ws=ws)
+    q = ops.linear_rope(x, P["wq"], qd, L, rope.cos, rope.sin, out=bufs.get("q", M, qd),
+                        norm=(P["n1"], eps))
     attn = bufs.get("attn", M, qd)
     ops.attention(q.view(B, L, qd), ck.view(B, Lc, -1), cv.view(B, Lc, -1), attn.view(B, L, qd),
                   cfg.n_q_heads, cfg.n_kv_heads, "none", 0)
-    ops.linear(attn, P["wo"], res=x, out=x, ws=ws)
-    _mlp(x, P, cfg, M, eps, bufs, ws)
+    ops.linear(attn, P["wo"], res=x, out=x)
+    _mlp(x, P, cfg, M, eps, bufs)
 
 
-def vit_layer(x, P, cfg: VitConfig, n_img, T, bufs: Optional[Buffers] = None, ws=None):
+def vit_layer(x, P, cfg: VitConfig, n_img, T, bufs: Optional[Buffers] = None):
     """SigLIP-style block on ``x [n_img*T, H]`` in place
     (vla/vision_block_bf16.py:308-420)."""
     bufs = bufs or Buffers(x.device)
     M = n_img * T
     H = cfg.hidden
     h = ops.layernorm(x, P["g1"], P["b1"], cfg.ln_eps, out=bufs.get("vh", M, H))
-    qkv = ops.linear(h, P["wqkv"], bias=P["bqkv"], out=bufs.get("vqkv", M, 3 * H), ws=ws)
+    qkv = ops.linear(h, P["wqkv"], bias=P["bqkv"], out=bufs.get("vqkv", M, 3 * H))
     q3 = qkv.view(n_img, T, 3 * H)
     attn = bufs.get("vattn", M, H)
     ops.attention(q3[:, :, :H], q3[:, :, H:2 * H], q3[:, :, 2 * H:], attn.view(n_img, T, H),
                   cfg.n_heads, cfg.n_heads, "none", 0, scale=1.0 / math.sqrt(cfg.head_dim))
-    ops.linear(attn, P["wo"], bias=P["bo"], res=x, out=x, ws=ws)
+    ops.linear(attn, P["wo"], bias=P["bo"], res=x, out=x)
     h = ops.layernorm(x, P["g2"], P["b2"], cfg.ln_eps, out=bufs.get("vh", M, H))
     act = ops.linear(h, P["wup"], bias=P["bup"], act="gelu_" + cfg.gelu,
-                     out=bufs.get("vmlp", M, cfg.inter), ws=ws)
-    ops.linear(act, P["wd"], bias=P["bd"], res=x, out=x, ws=ws)
+                     out=bufs.get("vmlp", M, cfg.inter))
+    ops.linear(act, P["wd"], bias=P["bd"], res=x, out=x)

@@ -22,8 +22,6 @@ F32 = torch.float32
 ACT = {None: 0, "none": 0, "gelu_tanh": 1, "tanh": 1, "gelu_erf": 2, "erf": 2, "silu": 3}
 MASK = {"none": 0, "causal": 1, "prefix_lm": 2}
 
-_WS = {}
-WS_BYTES = 64 << 20
 
 
 def _stream():
@@ -45,23 +43,13 @@ def _ld(t):
     return t.stride(0)
 
 
-def workspace(device=None) -> torch.Tensor:
-    """Per-device fp32 split-K workspace (allocated once, reused)."""
-    dev = torch.device(device or torch.cuda.current_device())
-    key = dev.index if dev.index is not None else torch.cuda.current_device()
-    ws = _WS.get(key)
-    if ws is None:
-        ws = torch.empty(WS_BYTES // 4, dtype=F32, device=dev)
-        _WS[key] = ws
-    return ws
-
-
-def _ws_args(ws):
-    if ws is False:
-        return None, 0
-    if ws is None:
-        ws = workspace()
-    return _ptr(ws), ws.numel() * 4
+def _norm_args(norm):
+    """``norm = (gain, eps)`` for a fused RMSNorm of the A rows, or None."""
+    if norm is None:
+        return None, 0.0
+    w, eps = norm
+    eps = torch.finfo(F32).eps if eps is None else eps
+    return _ptr(w), float(eps)
 
 
 # ----------------------------------------------------------------- norms ---
@@ -84,54 +72,54 @@ def layernorm(x, g, b, eps, out=None):
 
 # ------------------------------------------------------------------ GEMM ---
 def linear(a, w, bias=None, bias_f32=None, res=None, act=None, alpha=1.0, out=None,
-           out_f32=False, ws=None):
-    """``epilogue(alpha * a @ w.T)``; ``w`` packed ``[N, K]``."""
+           out_f32=False, norm=None):
+    """``epilogue(alpha * norm(a) @ w.T)``; ``w`` packed ``[N, K]``;
+    ``norm=(gain, eps)`` RMS-normalises the rows of ``a`` on the fly."""
     M, K = a.shape
     N = w.shape[0]
     if w.shape[1] != K:
         raise ValueError(f"linear: a {tuple(a.shape)} vs packed w {tuple(w.shape)}")
     if out is None:
         out = torch.empty(M, N, dtype=F32 if out_f32 else BF16, device=a.device)
-    wsp, wsb = _ws_args(ws)
+    nw, ne = _norm_args(norm)
     _lib.call("svla_linear_bf16", _ptr(a), _ld(a), _ptr(w), _ld(w), _ptr(bias), _ptr(bias_f32),
               _ptr(res), _ld(res) if res is not None else 0, _ptr(out), _ld(out), M, N, K,
-              float(alpha), ACT[act], int(out_f32), wsp, wsb, _stream())
+              float(alpha), ACT[act], int(out_f32), nw, ne, _stream())
     return out
 
 
-def linear_rope(a, w, rope_cols, seq_len, cos_t, sin_t, out=None, ws=None):
+def linear_rope(a, w, rope_cols, seq_len, cos_t, sin_t, out=None, norm=None):
     M, K = a.shape
     N = w.shape[0]
     out = torch.empty(M, N, dtype=BF16, device=a.device) if out is None else out
-    wsp, wsb = _ws_args(ws)
+    nw, ne = _norm_args(norm)
     _lib.call("svla_linear_rope_bf16", _ptr(a), _ld(a), _ptr(w), _ld(w), _ptr(out), _ld(out), M,
-              N, K, rope_cols, seq_len, _ptr(cos_t), _ptr(sin_t), wsp, wsb, _stream())
+              N, K, rope_cols, seq_len, _ptr(cos_t), _ptr(sin_t), nw, ne, _stream())
     return out
 
 
-def linear_silu_mul(a, w_gu, out=None, ws=None):
+def linear_silu_mul(a, w_gu, out=None, norm=None):
     M, K = a.shape
     inter = w_gu.shape[0] // 2
     out = torch.empty(M, inter, dtype=BF16, device=a.device) if out is None else out
-    wsp, wsb = _ws_args(ws)
+    nw, ne = _norm_args(norm)
     _lib.call("svla_linear_silu_mul_bf16", _ptr(a), _ld(a), _ptr(w_gu), _ld(w_gu), _ptr(out),
-              _ld(out), M, inter, K, wsp, wsb, _stream())
+              _ld(out), M, inter, K, nw, ne, _stream())
     return out
 
 
-def patch_embed(images, w, bias, pos, patch, out=None, ws=None):
+def patch_embed(images, w, bias, pos, patch, out=None):
     """``images [n, C, H, H]`` bf16 contiguous; ``w [E, C*P*P]``."""
     n, C, H, W = images.shape
     E = w.shape[0]
     G = H // patch
     out = torch.empty(n * G * G, E, dtype=BF16, device=images.device) if out is None else out
-    wsp, wsb = _ws_args(ws)
     _lib.call("svla_patch_embed_bf16", _ptr(images.contiguous()), _ptr(w), _ptr(bias), _ptr(pos),
-              _ptr(out), _ld(out), n, C, H, patch, E, wsp, wsb, _stream())
+              _ptr(out), _ld(out), n, C, H, patch, E, _stream())
     return out
 
 
-def connector(x, w, scale, out=None, rows_per_sample=0, sample_stride=0, ws=None):
+def connector(x, w, scale, out=None, rows_per_sample=0, sample_stride=0):
     """``x [n_img, grid*grid, hidden]`` contiguous -> ``[n_img*(grid/scale)^2, N]``
     (or remapped into a larger buffer, see ``svla_connector_bf16``)."""
     n, T, E = x.shape
@@ -143,19 +131,18 @@ def connector(x, w, scale, out=None, rows_per_sample=0, sample_stride=0, ws=None
         need = (rows // rows_per_sample - 1) * sample_stride + rows_per_sample
         if out.shape[0] < need:
             raise ValueError("connector: output buffer too small for the row remap")
-    wsp, wsb = _ws_args(ws)
     _lib.call("svla_connector_bf16", _ptr(x.contiguous()), _ptr(w), _ld(w), _ptr(out), _ld(out),
-              n, grid, E, scale, N, int(rows_per_sample), int(sample_stride), wsp, wsb,
-              _stream())
+              n, grid, E, scale, N, int(rows_per_sample), int(sample_stride), _stream())
     return out
 
 
-def action_out_euler(a, w, x_f32, dt, x_bf16=None):
+def action_out_euler(a, w, x_f32, dt, x_bf16=None, norm=None):
     M, K = a.shape
     N = w.shape[0]
+    nw, ne = _norm_args(norm)
     _lib.call("svla_action_out_euler", _ptr(a), _ld(a), _ptr(w), _ld(w), _ptr(x_f32),
               _ld(x_f32), _ptr(x_bf16), _ld(x_bf16) if x_bf16 is not None else 0, M, N, K,
-              float(dt), _stream())
+              nw, ne, float(dt), _stream())
     return x_f32
 
 
@@ -219,8 +206,7 @@ def rope(x, heads, cos_t, sin_t, pos_offset=0, out=None, out_f32=None):
         od = x.dtype if out_f32 is None else (F32 if out_f32 else BF16)
         out = torch.empty(rows, x.shape[1], dtype=od, device=x.device)
     _lib.call("svla_rope", _ptr(x), _ld(x), _ptr(out), _ld(out), rows, heads, _ptr(cos_t),
-              _ptr(sin_t), int(pos_offset), int(x.dtype == F32), int(out.dtype == F32),
-              _stream())
+              _ptr(sin_t), int(pos_offset), int(x.dtype == F32), int(out.dtype == F32), _stream())
     return out
 
 

@@ -98,13 +98,12 @@ class SmolVLAEngine:
         M = B * cfg.chunk
         self.x_t = z(M, cfg.action_dim, dt=F32)
         self.x_bf = z(M, cfg.action_dim)
-        self.temb = z(1, e.hidden)
-        self.tbias = z(1, e.hidden, dt=F32)
+        self.temb = z(cfg.num_steps, e.hidden)
+        self.tbias = z(cfg.num_steps, e.hidden, dt=F32)
         self.a_emb = z(M, e.hidden)
         self.h_time = z(M, e.hidden)
         self.ex = z(M, e.hidden)
         self.ebufs = layers.Buffers(dev)
-        self.ws = torch.empty(ops.WS_BYTES // 4, dtype=F32, device=dev)
         # materialise every lazily-named buffer before any capture
         self._forward()
         torch.cuda.synchronize(dev)
@@ -115,9 +114,9 @@ class SmolVLAEngine:
         v = cfg.vit
         nimg = self.B * cfg.n_cameras
         ops.patch_embed(self.in_images, self.patch_w, self.patch_b, self.pos_emb, v.patch,
-                        out=self.vit_x, ws=self.ws)
+                        out=self.vit_x)
         for P in self.vit:
-            layers.vit_layer(self.vit_x, P, v, nimg, v.tokens, self.vbufs, ws=self.ws)
+            layers.vit_layer(self.vit_x, P, v, nimg, v.tokens, self.vbufs)
 
     def build_prefix(self):
         cfg = self.cfg
@@ -127,19 +126,19 @@ class SmolVLAEngine:
         img_rows = cfg.n_cameras * cfg.image_tokens
         ops.connector(self.vit_x.view(nimg, cfg.vit.tokens, cfg.vit.hidden), self.conn_w,
                       cfg.pixel_shuffle, out=self.prefix_x, rows_per_sample=img_rows,
-                      sample_stride=L, ws=self.ws)
+                      sample_stride=L)
         ops.embed(self.in_ids, self.embed_table, math.sqrt(d.hidden), self.prefix_x[img_rows:],
                   per_sample=cfg.lang_tokens, out_bs=L * d.hidden)
         ops.f32_to_bf16(self.in_state, out=self.state_bf)
         st_rows = self.prefix_x.view(self.B, L, d.hidden)[:, L - 1, :]
-        ops.linear(self.state_bf, self.state_w, out=st_rows, ws=self.ws)
+        ops.linear(self.state_bf, self.state_w, out=st_rows)
 
     def run_prefix(self):
         cfg = self.cfg
         for P, kv in zip(self.prefix, self.kv):
             layers.decoder_layer(self.prefix_x, P, cfg.decoder, self.B, cfg.prefix_len,
                                  self.rope_prefix, cfg.prefix_mask, cfg.prefix_bidir_len,
-                                 self.pbufs, qkv_out=kv, ws=self.ws)
+                                 self.pbufs, qkv_out=kv)
 
     def project_cross(self):
         d = self.cfg.decoder
@@ -147,31 +146,37 @@ class SmolVLAEngine:
         for i, (ck, cv) in self.cross.items():
             kv = self.kv[i]
             layers.cross_kv(kv[:, qd:qd + kvd], kv[:, qd + kvd:], self.expert[i], out_k=ck,
-                            out_v=cv, ws=self.ws)
+                            out_v=cv)
 
-    def expert_step(self, t, dt):
+    def time_bias(self, ts):
+        """Time part of the action-time MLP input for every Euler step, hoisted
+        out of the loop (it depends on t only): tbias[s] = temb(t_s) @ W_time_in[H:]
+        + b_time_in, kept in fp32 so that the per-step GEMM rounds once as the
+        concatenated projection does."""
+        e = self.cfg.expert
+        for s, t in enumerate(ts):
+            ops.time_embedding(t, e.hidden, out=self.temb[s])
+        ops.linear(self.temb, self.w_tin_t, bias=self.b_tin, out=self.tbias, out_f32=True)
+
+    def expert_step(self, s, dt):
         cfg = self.cfg
         e = cfg.expert
         B, L, Lc = self.B, cfg.chunk, cfg.prefix_len
         # action / time embedding
-        ops.time_embedding(t, e.hidden, out=self.temb[0])
-        ops.linear(self.temb, self.w_tin_t, bias=self.b_tin, out=self.tbias, out_f32=True,
-                   ws=False)
-        ops.linear(self.x_bf, self.w_ain, bias=self.b_ain, out=self.a_emb, ws=self.ws)
-        ops.linear(self.a_emb, self.w_tin_a, bias_f32=self.tbias[0], act="silu",
-                   out=self.h_time, ws=self.ws)
-        ops.linear(self.h_time, self.w_tout, bias=self.b_tout, out=self.ex, ws=self.ws)
+        ops.linear(self.x_bf, self.w_ain, bias=self.b_ain, out=self.a_emb)
+        ops.linear(self.a_emb, self.w_tin_a, bias_f32=self.tbias[s], act="silu",
+                   out=self.h_time)
+        ops.linear(self.h_time, self.w_tout, bias=self.b_tout, out=self.ex)
         for i, P in enumerate(self.expert):
             if cfg.is_cross(i):
                 ck, cv = self.cross[i]
                 layers.cross_layer(self.ex, ck, cv, P, e, B, L, Lc, self.rope_expert,
-                                   self.ebufs, ws=self.ws)
+                                   self.ebufs)
             else:
                 layers.decoder_layer(self.ex, P, e, B, L, self.rope_expert, "causal", 0,
-                                     self.ebufs, ws=self.ws)
-        h = ops.rmsnorm(self.ex, self.n_exp, resolve_eps(e.rms_eps),
-                        out=self.ebufs.get("h", B * L, e.hidden))
-        ops.action_out_euler(h, self.w_aout, self.x_t, dt, x_bf16=self.x_bf)
+                                     self.ebufs)
+        ops.action_out_euler(self.ex, self.w_aout, self.x_t, dt, x_bf16=self.x_bf,
+                             norm=(self.n_exp, resolve_eps(e.rms_eps)))
 
     def _forward(self):
         cfg = self.cfg
@@ -182,10 +187,13 @@ class SmolVLAEngine:
         self.x_t.copy_(self.in_noise.view(-1, cfg.action_dim))
         ops.f32_to_bf16(self.x_t, out=self.x_bf)
         dt = -1.0 / cfg.num_steps
-        t = 1.0
+        ts, t = [], 1.0
         for _ in range(cfg.num_steps):
-            self.expert_step(t, dt)
+            ts.append(t)
             t = t + dt
+        self.time_bias(ts)
+        for s in range(cfg.num_steps):
+            self.expert_step(s, dt)
 
     # ------------------------------------------------------------ public ---
     def load_inputs(self, images, lang_ids, state, noise):
