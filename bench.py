@@ -106,7 +106,8 @@ def dominant_kernel_roofline(eng, iters):
     achieved = flops / (avg_ms * 1e-3) / 1e12
     hbm_bytes = 2.0 * (M * v.hidden + v.inter * v.hidden + M * v.inter + v.inter)
     return {
-        "kernel": "gemm_kernel<128,128,2,2,A_DENSE,EPI_STORE,GELU_TANH> (ViT MLP up-proj)",
+        "kernel": "gemm_pipe_kernel<0, false, 0, 1> (A_DENSE, no norm, EPI_STORE, GELU_TANH: "
+                  "ViT MLP up-projection)",
         "shape": [M, v.inter, v.hidden],
         "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),

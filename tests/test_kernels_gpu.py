@@ -129,6 +129,36 @@ def test_linear_bias_act_residual(ops):
     assert rel_err(got, want) < 1e-3
 
 
+@pytest.mark.parametrize("M,N,K", [(300, 260, 128), (1000, 700, 384), (513, 1028, 768),
+                                   (256, 256, 3072)])
+def test_wide_tile_forced(ops, force_tile, M, N, K):
+    """The 256x256 wide kernel (K % 128 == 0) on ragged M / N tails, through
+    the plain epilogues it serves: bias + GELU, bias + residual, alpha, fp32
+    out with fp32 bias."""
+    g = gen(M + N + K)
+    force_tile(8)
+    a, w, b = randn(g, M, K), randn(g, K, N, std=0.05), randn(g, N, std=0.05)
+    wp = ops.pack_weight(w.cuda())
+    assert_close_bf16(ops.linear(a.cuda(), wp, bias=b.cuda(), act="gelu_tanh"),
+                      ref.gelu(ref.linear(a, w, b), "tanh"))
+    res = randn(g, M, N)
+    assert_close_bf16(ops.linear(a.cuda(), wp, bias=b.cuda(), res=res.cuda()),
+                      ref.linear(a, w, b) + res)
+    assert_close_bf16(ops.linear(a.cuda(), wp, alpha=0.125), (ref.linear(a, w).float() * 0.125))
+    bf = torch.randn(N, generator=g) * 0.1
+    got = ops.linear(a.cuda(), wp, bias_f32=bf.cuda(), out_f32=True)
+    assert rel_err(got, a.float() @ w.float() + bf) < 1e-3
+
+
+def test_wide_tile_auto_vit_up(ops):
+    # a ViT MLP up-projection large enough for the automatic wide-tile choice
+    g = gen(17)
+    M, N, K = 16384, 3072, 768
+    a, w, b = randn(g, M, K), randn(g, K, N, std=0.02), randn(g, N, std=0.02)
+    got = ops.linear(a.cuda(), ops.pack_weight(w.cuda()), bias=b.cuda(), act="gelu_tanh")
+    assert_close_bf16(got, ref.gelu(ref.linear(a, w, b), "tanh"))
+
+
 def test_linear_gelu_big_tile(ops):
     # the ViT MLP up-projection shape class on the 256x256 tile
     g = gen(13)
@@ -168,6 +198,60 @@ def test_fused_rmsnorm_prologue(ops, M, K):
     got = ops.linear_silu_mul(x.cuda(), wgu, norm=(nw.cuda(), 1e-5))
     sep = ops.linear_silu_mul(ops.rmsnorm(x.cuda(), nw.cuda(), 1e-5), wgu)
     same(got, sep)
+
+
+TILES = {0: "256x256/32", 1: "128x128/32", 2: "64x128/16", 3: "64x64/16", 4: "skinny64",
+         5: "skinny32", 6: "128x128/16", 7: "pipe128", 8: "wide256"}
+
+
+@pytest.fixture
+def force_tile(ops):
+    from smolvla import _lib
+    lib = _lib.load()
+    yield lambda t: lib.svla_gemm_set_tile(t)
+    lib.svla_gemm_set_tile(-1)
+
+
+@pytest.mark.parametrize("tile", sorted(TILES))
+def test_every_tile_config_every_epilogue(ops, force_tile, tile):
+    """Each GEMM kernel configuration, forced, on ragged shapes (M, N, K
+    tails) through every epilogue, the fused RMSNorm and both A gathers."""
+    g = gen(100 + tile)
+    force_tile(tile)
+    M, K = 200, 200                                   # K tail (200 = 6*32 + 8)
+    x = randn(g, M, K)
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16)
+    # plain + bias + GELU, residual, fp32 out
+    w, b = randn(g, K, 260, std=0.05), randn(g, 260, std=0.05)
+    wp = ops.pack_weight(w.cuda())
+    assert_close_bf16(ops.linear(x.cuda(), wp, bias=b.cuda(), act="gelu_tanh"),
+                      ref.gelu(ref.linear(x, w, b), "tanh"))
+    res = randn(g, M, 260)
+    assert_close_bf16(ops.linear(x.cuda(), wp, res=res.cuda()), ref.linear(x, w) + res)
+    assert_close_bf16(ops.linear(x.cuda(), wp, norm=(nw.cuda(), 1e-5)),
+                      ref.linear(ref.rms_norm(x, nw, 1e-5), w))
+    if tile != 5:                                      # paired epilogues need 64-wide tiles
+        wq = randn(g, K, 192, std=0.05)
+        c, s_ = ops.rope_table(40, 64, 1e4)
+        got = ops.linear_rope(x.cuda(), ops.pack_weight(wq.cuda()), 128, 40, c, s_,
+                              norm=(nw.cuda(), 1e-5)).cpu()
+        h = ref.rms_norm(x, nw, 1e-5)
+        qk = ref.apply_rope(ref.linear(h, wq[:, :128]).view(5, 40, 2, 64), 1e4).to(BF16)
+        assert_close_bf16(got[:, :128], qk.view(M, 128))
+        assert_close_bf16(got[:, 128:], ref.linear(h, wq[:, 128:]))
+        wg, wu = randn(g, K, 96, std=0.05), randn(g, K, 96, std=0.05)
+        got = ops.linear_silu_mul(x.cuda(), ops.pack_gate_up(wg.cuda(), wu.cuda()))
+        assert_close_bf16(got, ref.silu(ref.linear(x, wg)) * ref.linear(x, wu))
+    # gathers: im2col patch embedding (2 images of 64x64) and pixel shuffle
+    img = (torch.rand(2, 3, 64, 64, generator=g) * 2 - 1).to(BF16)
+    kern, kb = randn(g, 96, 3, 16, 16, std=0.05), randn(g, 96, std=0.05)
+    pos = randn(g, 16, 96, std=0.05)
+    got = ops.patch_embed(img.cuda(), kern.reshape(96, -1).cuda(), kb.cuda(), pos.cuda(), 16)
+    assert_close_bf16(got, ref.patch_embed(img, kern, kb, pos).reshape(-1, 96))
+    xv = randn(g, 2, 64, 96)
+    wc = randn(g, 96 * 4, 64, std=0.05)
+    got = ops.connector(xv.cuda(), ops.pack_weight(wc.cuda()), 2)
+    assert_close_bf16(got, ref.connector(xv, wc, 2).reshape(-1, 64))
 
 
 def test_repeated_calls_deterministic(ops):

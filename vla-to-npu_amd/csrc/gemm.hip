@@ -436,6 +436,389 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
   }
 }
 
+// ---- pipelined large-tile GEMM (LDS DMA) --------------------------------------
+// 128x128 block tile, K step 32, 4-stage ring of LDS buffers filled by
+// global_load_lds_dwordx4 (each instruction moves 64 lanes x 16 B straight
+// into LDS, no register staging), so three K tiles are in flight while the
+// fourth is multiplied.  The stages are separate LDS variables and every DMA
+// is issued unconditionally (addresses clamped into the tensors), which lets
+// the compiler track each stage's DMA separately instead of draining all of
+// them before every LDS read; the only waits are the explicit vmcnt(8)
+// before each barrier (two newer stages stay in flight).
+// LDS layout of a stage: row r holds 4 chunks of 8 bf16; logical chunk g of
+// row r sits in slot g ^ ((r >> 1) & 3), so the 16-byte fragment reads of 8
+// consecutive rows fall in 8 distinct bank groups.
+constexpr int PBM = 128, PBN = 128, PBK = 32, PST = 4;
+constexpr int P_DMA = 2;  // 1 KB DMA blocks per wave per operand per stage
+
+__device__ __forceinline__ int pswz(int r, int g) { return g ^ ((r >> 1) & 3); }
+
+template <int AMODE, bool NORM, int EPI, int ACT>
+__global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
+  __shared__ __attribute__((aligned(1024))) bf16 sA0[PBM * PBK], sA1[PBM * PBK],
+      sA2[PBM * PBK], sA3[PBM * PBK];
+  __shared__ __attribute__((aligned(1024))) bf16 sB0[PBN * PBK], sB1[PBN * PBK],
+      sB2[PBN * PBK], sB3[PBN * PBK];
+  __shared__ float s_rs[NORM ? PBM : 1];
+  __shared__ __attribute__((aligned(16))) bf16 s_gain[NORM ? 2048 : 8];  // norm gain (K <= 2048)
+  constexpr int TM = 4, TN = 4;  // wave tile 64 x 64 of 16x16 MFMA tiles
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int gn = gridDim.x;
+  const int tile = xcd_remap(blockIdx.y * gn + blockIdx.x, gn * gridDim.y);
+  const int tm_idx = tile / gn, tn_idx = tile - tm_idx * gn;
+  const int m0 = tm_idx * PBM, n0 = tn_idx * PBN;
+  const int nk = (p.K + PBK - 1) / PBK;
+
+  if constexpr (NORM) {
+    for (int r = wave; r < PBM; r += 4) {
+      const int m = m0 + r;
+      float ss = 0.f;
+      if (m < p.M) {
+        const bf16* xr = p.a + (long)m * p.lda;
+        for (int c = lane * 8; c < p.K; c += 512) {
+          const bf16x8 v = ld8(xr + c);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            const float f = bf2f(v[j]);
+            ss += f * f;
+          }
+        }
+      }
+      ss = wave_sum(ss);
+      if (lane == 0) s_rs[r] = 1.0f / sqrtf(ss / (float)p.K + p.norm_eps);
+    }
+    // the gain vector lives in LDS so the main loop issues no global loads
+    // besides its DMA (a plain load would force a full vmcnt drain)
+    for (int c = tid * 8; c < p.K; c += 256 * 8)
+      *reinterpret_cast<bf16x8*>(&s_gain[c]) = ld8(p.norm_w + c);
+    __syncthreads();
+  }
+
+  // per-lane DMA source rows (fixed across K tiles): block b = wave*P_DMA + j
+  // covers rows 16b .. 16b+15, lane -> row 16b + lane/4, slot lane%4
+  int a_row[P_DMA], b_row[P_DMA], slot_g[P_DMA];
+#pragma unroll
+  for (int j = 0; j < P_DMA; ++j) {
+    const int r = (wave * P_DMA + j) * 16 + (lane >> 2);
+    a_row[j] = min(m0 + r, p.M - 1);
+    b_row[j] = min(n0 + r, p.N - 1);
+    slot_g[j] = pswz(r, lane & 3);
+  }
+
+  auto issue = [&](auto SI, int kt) {
+    constexpr int S = decltype(SI)::value;
+    bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
+    bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
+    kt = min(kt, nk - 1);  // past the end: reload the last tile (never read)
+#pragma unroll
+    for (int j = 0; j < P_DMA; ++j) {
+      const int blk = wave * P_DMA + j;
+      const int k = kt * PBK + slot_g[j] * 8;
+      const bf16* ga;
+      if constexpr (AMODE == A_DENSE) ga = p.a + (long)a_row[j] * p.lda + k;
+      else {
+        // gathers: load_a's address map, clamped to a valid element
+        const bf16* base = nullptr;
+        if constexpr (AMODE == A_PSHUF) {
+          const int s_ = p.g_scale, E = p.g_hidden, grid = p.g_grid, gs = grid / s_;
+          const int per = gs * gs, mm = a_row[j];
+          const int img = mm / per, i = mm - img * per, hp = i / gs, wp = i - hp * gs;
+          const int sE = s_ * E, t = k / sE, rem = k - t * sE, u = rem / E, c = rem - u * E;
+          base = p.a + ((long)img * grid * grid + (long)(s_ * hp + t) * grid + s_ * wp + u) * E + c;
+        } else {
+          const int P = p.p_patch, H = p.p_img, G = H / P, per = G * G, mm = a_row[j];
+          const int img = mm / per, tkn = mm - img * per, pr = tkn / G, pc = tkn - pr * G;
+          const int P2 = P * P, ch = k / P2, r = k - ch * P2, ky = r / P, kx = r - ky * P;
+          base = p.a + (((long)img * p.p_chans + ch) * H + pr * P + ky) * H + pc * P + kx;
+        }
+        ga = base;
+      }
+      __builtin_amdgcn_global_load_lds((void*)ga, (lds_ptr_t)(sa + blk * 512), 16, 0, 0);
+      const bf16* gb = p.b + (long)b_row[j] * p.ldb + k;
+      __builtin_amdgcn_global_load_lds((void*)gb, (lds_ptr_t)(sb + blk * 512), 16, 0, 0);
+    }
+  };
+
+  f32x4 acc[TN][TM];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int fr = lane & 15, g = lane >> 4;
+  float rs[TM];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) rs[tm] = s_rs[wm * 64 + tm * 16 + fr];
+  }
+
+  auto compute = [&](auto SI, int kt) {
+    constexpr int S = decltype(SI)::value;
+    const bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
+    const bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
+    const int k = kt * PBK + g * 8;  // K % PBK == 0: no tail to mask
+    bf16x8 fw[TN], fx[TM];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int r = wn * 64 + tn * 16 + fr;
+      fw[tn] = *reinterpret_cast<const bf16x8*>(&sb[r * PBK + pswz(r, g) * 8]);
+    }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      const int r = wm * 64 + tm * 16 + fr;
+      fx[tm] = *reinterpret_cast<const bf16x8*>(&sa[r * PBK + pswz(r, g) * 8]);
+    }
+    if constexpr (NORM) {
+      const bf16x8 gw = *reinterpret_cast<const bf16x8*>(&s_gain[k]);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          fx[tm][j] = f2bf(__fmul_rn(__fmul_rn(bf2f(fx[tm][j]), rs[tm]), bf2f(gw[j])));
+    }
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+        acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[tn], fx[tm], acc[tn][tm], 0, 0, 0);
+  };
+
+  // s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained: each stage
+  // is P_DMA * 2 DMA instructions per wave and two newer stages may stay in
+  // flight, so N = 2 * P_DMA * 2 (gfx9 encoding: vmcnt[3:0] in bits 3:0,
+  // expcnt = 7 in bits 6:4, lgkmcnt = 15 in bits 11:8)
+  constexpr int kWaitN = 2 * P_DMA * 2;
+  static_assert(kWaitN <= 15, "vmcnt immediate");
+  constexpr int kWait2 = 0xF70 | kWaitN;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+
+  issue(I0{}, 0);
+  issue(I1{}, 1);
+  issue(I2{}, 2);
+  for (int kt = 0; kt < nk; kt += PST) {
+    __builtin_amdgcn_s_waitcnt(kWait2);
+    __builtin_amdgcn_s_barrier();
+    issue(I3{}, kt + 3);
+    compute(I0{}, kt);
+    __builtin_amdgcn_s_waitcnt(kWait2);
+    __builtin_amdgcn_s_barrier();
+    issue(I0{}, kt + 4);
+    if (kt + 1 < nk) compute(I1{}, kt + 1);
+    __builtin_amdgcn_s_waitcnt(kWait2);
+    __builtin_amdgcn_s_barrier();
+    issue(I1{}, kt + 5);
+    if (kt + 2 < nk) compute(I2{}, kt + 2);
+    __builtin_amdgcn_s_waitcnt(kWait2);
+    __builtin_amdgcn_s_barrier();
+    issue(I2{}, kt + 6);
+    if (kt + 3 < nk) compute(I3{}, kt + 3);
+  }
+  // drain the trailing (never read) DMA before the workgroup can exit
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // ---- epilogue (same lane layout as gemm_kernel with MF = 16)
+  const int col_in = 4 * g;
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) {
+    const int m = m0 + wm * 64 + tm * 16 + fr;
+    if (m >= p.M) continue;
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int n = n0 + wn * 64 + tn * 16 + col_in;
+      if constexpr (EPI == EPI_ROPE || EPI == EPI_SILU) {
+        if (tn >= 2 || n >= p.N) continue;
+        float x1[4], x2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x1[i] = acc[tn][tm][i] * p.alpha;
+          x2[i] = acc[tn + 2][tm][i] * p.alpha;
+        }
+        if constexpr (EPI == EPI_ROPE) epi_rope(p, m, n, x1, x2);
+        else epi_silu(p, m, n, x1, x2);
+      } else {
+        if (n >= p.N) continue;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][i] * p.alpha;
+        if constexpr (EPI == EPI_EULER) epi_euler(p, m, n, v);
+        else epi_store<ACT>(p, m, n, v);
+      }
+    }
+  }
+}
+
+// ---- wide GEMM: 256 x 256 block tile, one workgroup per CU -------------------
+// For the big-M problems (the batched ViT, M = 98304 rows at batch 32).  Each
+// of the 4 waves owns a 128 x 128 output tile (8 x 8 MFMA 16x16x32 tiles, 256
+// fp32 accumulators per lane, kept in AGPRs), which halves the LDS bytes read
+// per MFMA FLOP relative to a 64 x 64 wave tile: 16 fragment reads feed 64
+// MFMAs per K step.  Operands stream through a 4-stage ring of LDS buffers
+// (K step 32, 32 KB per stage, 128 KB in total) filled by global_load_lds.
+// The barrier of step s guarantees stage s + 1 is in LDS, so the fragments of
+// step s + 1 are read into a second register set while the MFMAs of step s
+// run and no LDS latency is exposed; the DMA and fragment reads are spread
+// between the MFMAs.  One barrier per K step, three stages of DMA in flight.
+// Same LDS row swizzle and accumulator layout as gemm_pipe_kernel.
+//
+// The MFMAs are issued through inline asm with the accumulator tied to an
+// AGPR operand: with the builtin, the register allocator shuffles AGPR-resident
+// loop accumulators with v_accvgpr_mov copies every iteration (measured: more
+// than half of the MFMA rate lost).  The asm is opaque to the hazard
+// recognizer, so the kernel inserts the wait states itself: before the first
+// MFMA reads the zeroed accumulators and before the epilogue reads results.
+constexpr int WBM = 256, WBN = 256, WBK = 32;
+constexpr int W_DMA = 4;  // 1 KB DMA blocks per wave per operand per stage
+constexpr int WTM = 8, WTN = 8;  // wave tile 128 x 128 = 8 x 8 MFMA tiles
+
+// s_waitcnt immediate (gfx9 encoding): vmcnt split over bits 3:0 and 15:14,
+// expcnt bits 6:4 (7 = no wait), lgkmcnt bits 11:8 (15 = no wait)
+constexpr int waitcnt_imm(int vm, int lgkm) {
+  return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
+}
+
+__device__ __forceinline__ void mfma_agpr(f32x4& acc, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+
+template <int AMODE, bool NORM, int EPI, int ACT>
+__global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
+  static_assert(AMODE == A_DENSE && !NORM && EPI == EPI_STORE, "wide tile: plain dense GEMM");
+  __shared__ __attribute__((aligned(1024))) bf16 sA0[WBM * WBK], sA1[WBM * WBK],
+      sA2[WBM * WBK], sA3[WBM * WBK];
+  __shared__ __attribute__((aligned(1024))) bf16 sB0[WBN * WBK], sB1[WBN * WBK],
+      sB2[WBN * WBK], sB3[WBN * WBK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int gn = gridDim.x;
+  const int tile = xcd_remap(blockIdx.y * gn + blockIdx.x, gn * gridDim.y);
+  const int tm_idx = tile / gn, tn_idx = tile - tm_idx * gn;
+  const int m0 = tm_idx * WBM, n0 = tn_idx * WBN;
+  const int nk = p.K / WBK;  // K % (4 * WBK) == 0 (checked by the launcher)
+
+  // per-lane DMA sources: block b = wave * W_DMA + j covers rows 16b .. 16b+15;
+  // lane -> row 16b + lane / 4, LDS slot lane % 4 holding logical chunk
+  // pswz(row, slot).  Rows past M / N are clamped (their results are dropped).
+  const bf16* a_src[W_DMA];
+  const bf16* b_src[W_DMA];
+#pragma unroll
+  for (int j = 0; j < W_DMA; ++j) {
+    const int r = (wave * W_DMA + j) * 16 + (lane >> 2);
+    const int g = pswz(r, lane & 3);
+    a_src[j] = p.a + (long)min(m0 + r, p.M - 1) * p.lda + g * 8;
+    b_src[j] = p.b + (long)min(n0 + r, p.N - 1) * p.ldb + g * 8;
+  }
+
+  // DMA j of a stage: j < W_DMA -> A block, else B block j - W_DMA
+  auto issue_one = [&](auto SI, int j, int kt) {
+    constexpr int S = decltype(SI)::value;
+    bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
+    bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
+    const int k = min(kt, nk - 1) * WBK;  // past the end: reload the last tile (never read)
+    if (j < W_DMA)
+      __builtin_amdgcn_global_load_lds((void*)(a_src[j] + k),
+                                       (lds_ptr_t)(sa + (wave * W_DMA + j) * 512), 16, 0, 0);
+    else
+      __builtin_amdgcn_global_load_lds((void*)(b_src[j - W_DMA] + k),
+                                       (lds_ptr_t)(sb + (wave * W_DMA + j - W_DMA) * 512), 16, 0, 0);
+  };
+  auto issue = [&](auto SI, int kt) {
+#pragma unroll
+    for (int j = 0; j < 2 * W_DMA; ++j) issue_one(SI, j, kt);
+  };
+
+  f32x4 acc[WTN][WTM];
+#pragma unroll
+  for (int i = 0; i < WTN; ++i)
+#pragma unroll
+    for (int j = 0; j < WTM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // fragment f of a stage: f < WTN -> weight tile f, else activation tile f - WTN
+  const int fr = lane & 15, g = lane >> 4;
+  const int frag_off = fr * WBK + pswz(fr, g) * 8;  // pswz depends on fr only
+  bf16x8 fw[2][WTN], fx[2][WTM];
+  auto read_one = [&](auto SI, auto RI, int f) {
+    constexpr int S = decltype(SI)::value, R = decltype(RI)::value;
+    const bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
+    const bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
+    if (f < WTN)
+      fw[R][f] = *reinterpret_cast<const bf16x8*>(&sb[(wn * 128 + f * 16) * WBK + frag_off]);
+    else
+      fx[R][f - WTN] =
+          *reinterpret_cast<const bf16x8*>(&sa[(wm * 128 + (f - WTN) * 16) * WBK + frag_off]);
+  };
+
+  // each stage is 2 * W_DMA DMA instructions per wave
+  constexpr int kStageVm = 2 * W_DMA;
+  constexpr int kWaitPrologue = waitcnt_imm(3 * kStageVm, 15);  // stage 0 landed
+  constexpr int kWaitStep = waitcnt_imm(2 * kStageVm, 0);       // next stage landed, own reads done
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+
+  // One step of the ring: wait until stage s + 1 is in LDS for every wave and
+  // every wave holds its stage-s fragments, then, between the first 32 of the
+  // 64 MFMAs of stage s: refill stage s's buffer with K tile s + 4 (one DMA
+  // every 4 MFMAs) and read stage s + 1's fragments into the other register
+  // set (one every 2 MFMAs), so the reads have landed by the next step.
+  auto step = [&](auto SI, auto SN, auto RC, int kt) {
+    constexpr int R = decltype(RC)::value;
+    using RN = std::integral_constant<int, 1 - R>;
+    __builtin_amdgcn_s_waitcnt(kWaitStep);
+    __builtin_amdgcn_s_barrier();
+#pragma unroll
+    for (int i = 0; i < WTN * WTM; ++i) {
+      mfma_agpr(acc[i / WTM][i % WTM], fw[R][i / WTM], fx[R][i % WTM]);
+      if (i < 32 && i % 4 == 0) issue_one(SI, i / 4, kt + 4);
+      if (i < 32 && i % 2 == 1) read_one(SN, RN{}, i / 2);
+    }
+  };
+
+  // zeroed accumulators are written by VALU; the first MFMA reads them as srcC
+  asm volatile("s_nop 4");
+  issue(I0{}, 0);
+  issue(I1{}, 1);
+  issue(I2{}, 2);
+  issue(I3{}, 3);
+  __builtin_amdgcn_s_waitcnt(kWaitPrologue);
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int f = 0; f < WTN + WTM; ++f) read_one(I0{}, I0{}, f);
+  for (int kt = 0; kt < nk; kt += 4) {  // nk % 4 == 0 (checked by the launcher)
+    step(I0{}, I1{}, I0{}, kt);
+    step(I1{}, I2{}, I1{}, kt + 1);
+    step(I2{}, I3{}, I0{}, kt + 2);
+    step(I3{}, I0{}, I1{}, kt + 3);
+  }
+  // drain the trailing (never read) DMA and fragment reads before exit, and
+  // let the last MFMAs retire before their accumulators are read
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+
+  // ---- epilogue: lane holds C[m][n .. n+3], m = row fr of MFMA tile tm,
+  // n = 4 * g within MFMA tile tn
+#pragma unroll
+  for (int tn = 0; tn < WTN; ++tn) {
+    const int n = n0 + wn * 128 + tn * 16 + 4 * g;
+    if (n >= p.N) continue;
+#pragma unroll
+    for (int tm = 0; tm < WTM; ++tm) {
+      const int m = m0 + wm * 128 + tm * 16 + fr;
+      if (m >= p.M) continue;
+      float v[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][i] * p.alpha;
+      epi_store<ACT>(p, m, n, v);
+    }
+  }
+}
+
 // ---- skinny-M GEMM ----------------------------------------------------------
 // One workgroup = 64 rows x BN columns, 8 waves.  The waves split the K loop
 // (in steps of 32) and each accumulates the whole tile with 16x16x32 MFMAs
@@ -616,7 +999,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
 
 // ---- launch ---------------------------------------------------------------
 enum TileId { T256 = 0, T128 = 1, T64x128 = 2, T64 = 3, S64 = 4, S32 = 5, T128S = 6,
-              NUM_TILES = 7 };
+              P128 = 7, W256 = 8, NUM_TILES = 9 };
 
 template <int AMODE, bool NORM, int EPI, int ACT>
 void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
@@ -638,6 +1021,13 @@ void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
       break;
     case S64:
       hipLaunchKernelGGL((skinny_kernel<64, AMODE, NORM, EPI, ACT>), grid, dim3(SK_WAVES * 64), 0, s, p);
+      break;
+    case P128:
+      hipLaunchKernelGGL((gemm_pipe_kernel<AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      break;
+    case W256:
+      if constexpr (AMODE == A_DENSE && !NORM && EPI == EPI_STORE)
+        hipLaunchKernelGGL((gemm_wide_kernel<AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
       break;
     default:
       if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
@@ -661,6 +1051,8 @@ TileCfg tile_dims(TileId id) {
     case T256: return {T256, 256, 256};
     case T128: return {T128, 128, 128};
     case T128S: return {T128S, 128, 128};
+    case P128: return {P128, 128, 128};
+    case W256: return {W256, 256, 256};
     case T64x128: return {T64x128, 64, 128};
     case T64: return {T64, 64, 64};
     case S64: return {S64, 64, 64};
@@ -668,18 +1060,28 @@ TileCfg tile_dims(TileId id) {
   }
 }
 
-TileCfg pick_tile(int M, int N, int epi) {
+// `plain`: dense A, no fused norm, plain store epilogue (the wide kernel's scope)
+TileCfg pick_tile(int M, int N, int K, int epi, bool plain) {
   auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-  const bool paired_ = epi == EPI_ROPE || epi == EPI_SILU;
-  if (g_force_tile >= 0 && !(paired_ && g_force_tile == S32)) return tile_dims((TileId)g_force_tile);
   const bool paired = epi == EPI_ROPE || epi == EPI_SILU;
+  const bool pipe_ok = K % PBK == 0;  // the pipelined kernels have no K tail
+  const bool wide_ok = plain && K % (4 * WBK) == 0;  // whole 4-stage rounds
+  if (g_force_tile >= 0 && !(paired && g_force_tile == S32)) {
+    if (g_force_tile == W256 && !wide_ok) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
+    if (g_force_tile == P128 && !pipe_ok) return tile_dims(T128);
+    return tile_dims((TileId)g_force_tile);
+  }
   if (M <= kSkinnyMaxM) {
     if (!paired && tiles(64, 64) < kNumCU / 2) return {S32, 64, 32};
     return {S64, 64, 64};
   }
   // measured on MI355X: 128x128 tiles win once the grid has ~4 waves of
   // workgroups; below that the 64x64 tile's larger grid wins
-  if (M >= 4096 || tiles(128, 128) >= 4 * kNumCU) return {T128, 128, 128};
+  // measured on MI355X (M = 98304): the wide tile wins at K = 3072 (+21%) and
+  // ties or loses at K = 768, where its per-tile pipeline fill and epilogue
+  // weigh more
+  if (wide_ok && K >= 1536 && tiles(WBM, WBN) >= 2 * kNumCU) return tile_dims(W256);
+  if (M >= 4096 || tiles(128, 128) >= 4 * kNumCU) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
   return {T64, 64, 64};
 }
 
@@ -714,7 +1116,8 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
   if (AMODE != A_DENSE && act) return SVLA_EINVAL;
   if (p.norm_w && (AMODE != A_DENSE || !svla_aligned16(p.norm_w))) return SVLA_EINVAL;
 
-  const TileCfg t = pick_tile(p.M, p.N, epi);
+  const bool plain = AMODE == A_DENSE && !p.norm_w && epi == EPI_STORE;
+  const TileCfg t = pick_tile(p.M, p.N, p.K, epi, plain);
   if (p.norm_w && p.K > 2048) return SVLA_EINVAL;  // row statistics keep <= 2048 per row
   const int gm = (p.M + t.bm - 1) / t.bm, gn = (p.N + t.bn - 1) / t.bn;
   dim3 grid(gn, gm, 1);

@@ -19,6 +19,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+// LDS pointer type for __builtin_amdgcn_global_load_lds destinations
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 #define SVLA_WAVE 64
 
@@ -43,14 +45,28 @@ __device__ __forceinline__ float wave_max(float v) {
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 __device__ __forceinline__ void st8(bf16* p, bf16x8 v) { *reinterpret_cast<bf16x8*>(p) = v; }
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + __expf(-x)); }
+// x * sigmoid(x) as x / (1 + 2^(-x log2 e)) with the hardware exp2 and
+// reciprocal (1 ulp each): the result is rounded to bf16 by every caller, so
+// the IEEE division's extra accuracy is invisible.  exp2 -> inf for very
+// negative x gives x * 0 = -0, the correctly rounded limit.
+__device__ __forceinline__ float fast_sigmoid_scaled(float z_log2e) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-z_log2e));
+}
+__device__ __forceinline__ float silu_f(float x) {
+  return x * fast_sigmoid_scaled(x * 1.4426950408889634f);
+}
 
-// tanh-approximated GELU, computed as torch does for approximate='tanh':
-// 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))).
+// tanh-approximated GELU (torch approximate='tanh'):
+//   0.5 x (1 + tanh(u)),  u = sqrt(2/pi) (x + 0.044715 x^3)
+// evaluated through the identity 0.5 (1 + tanh(u)) = sigmoid(2u), i.e.
+//   x / (1 + exp(-2u)),
+// which needs one exp2 and one reciprocal instead of a tanh (the tanh form
+// also loses all relative accuracy for x < -3 where 1 + tanh(u) cancels).
 __device__ __forceinline__ float gelu_tanh_f(float x) {
-  const float k0 = 0.7978845608028654f, k1 = 0.044715f;
-  float inner = k0 * (x + k1 * x * x * x);
-  return 0.5f * x * (1.0f + tanhf(inner));
+  // 2 * sqrt(2/pi) * log2(e) and 2 * sqrt(2/pi) * 0.044715 * log2(e)
+  const float c0 = 2.3022082f, c1 = 0.10294324f;
+  const float z = x * __builtin_fmaf(c1, x * x, c0);
+  return x * fast_sigmoid_scaled(z);
 }
 
 // exact-erf GELU (the reference's nn.GELU() default)
