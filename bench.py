@@ -105,6 +105,8 @@ def dominant_kernel_roofline(eng, iters):
     flops = 2.0 * M * v.inter * v.hidden
     achieved = flops / (avg_ms * 1e-3) / 1e12
     hbm_bytes = 2.0 * (M * v.hidden + v.inter * v.hidden + M * v.inter + v.inter)
+    tr = load_traffic()
+    traffic = tr.get("bytes_per_launch") if tr and tr.get("shape") == [M, v.inter, v.hidden] else None
     return {
         "kernel": "gemm_pipe_kernel<0, false, 0, 1> (A_DENSE, no norm, EPI_STORE, GELU_TANH: "
                   "ViT MLP up-projection)",
@@ -112,8 +114,45 @@ def dominant_kernel_roofline(eng, iters):
         "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
         "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_bytes": hbm_bytes,
-        "traffic": None,
+        "traffic": traffic,
     }
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "dominant_kernel_traffic.json"
+
+
+def traffic_probe(cfg, batch):
+    """Counter-collection entry point (run under ``rocprofv3 --pmc FETCH_SIZE``
+    and again under ``--pmc WRITE_SIZE``): the dominant kernel alone at its
+    batch-``batch`` shape, 3 launches, then a plain 1 GiB device copy, 3
+    launches, whose known byte count calibrates the counters."""
+    from smolvla import ops
+    v = cfg.vit
+    M = batch * cfg.n_cameras * v.tokens
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(M, v.hidden, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(v.inter, v.hidden, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(v.inter, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    out = torch.empty(M, v.inter, device="cuda", dtype=torch.bfloat16)
+    for _ in range(3):
+        ops.linear(x, w, bias=b, act="gelu_" + v.gelu, out=out)
+    src = torch.ones(1 << 29, device="cuda", dtype=torch.bfloat16)   # 1 GiB
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"traffic probe done: GEMM {M}x{v.inter}x{v.hidden}, copy 1 GiB")
+
+
+def load_traffic():
+    """HBM bytes per launch of the dominant kernel, measured by the
+    FETCH_SIZE / WRITE_SIZE counter runs of ``--traffic-probe`` (scaled by the
+    copy calibration) and committed with their rocprofv3 summary; None when
+    absent."""
+    try:
+        return json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
 
 
 def cpu_baseline(cfg, params, seconds):
@@ -150,6 +189,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-latency", action="store_true")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only launch the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs on a single GPU "
@@ -162,6 +203,9 @@ def main():
     from smolvla.pipeline import SmolVLAEngine
 
     cfg = SmolVLAConfig()
+    if args.traffic_probe:
+        traffic_probe(cfg, args.batch)
+        return
     log("generating seeded random-init bf16 weights")
     params = smolvla_params(cfg, seed=0)
     B = args.batch

@@ -240,13 +240,30 @@ constexpr int BK = 64;
 constexpr int LDS_STRIDE = BK + 8;  // elements; +16 bytes of padding per row
 constexpr int kNumXCD = 8;
 
-// Maps the hardware workgroup id so that consecutive logical tiles (n fastest)
-// share an XCD.
+// Maps the hardware workgroup id so that consecutive logical tiles share an
+// XCD (the hardware deals workgroups round-robin over the 8 XCDs).
 __device__ __forceinline__ int xcd_remap(int bid, int total) {
   const int per = total / kNumXCD;
   const int full = per * kNumXCD;
   if (bid >= full) return bid;
   return (bid % kNumXCD) * per + bid / kNumXCD;
+}
+
+// Logical tile -> (row block, column block) in groups of kGroupRows row
+// blocks: consecutive tiles walk down a group's rows, then across its
+// columns, so the workgroups that run together on one XCD cover a compact
+// rows x columns patch and share both their A row panels and their weight
+// column panels in that XCD's L2.  (Row-major order makes a concurrent set
+// span every column block, i.e. the whole weight matrix, which does not fit.)
+constexpr int kGroupRows = 8;
+__device__ __forceinline__ void tile_coords(int t, int gm, int gn, int& tm, int& tn) {
+  const int per_group = kGroupRows * gn;
+  const int group = t / per_group;
+  const int first = group * kGroupRows;
+  const int rows = min(gm - first, kGroupRows);
+  const int r = t - group * per_group;
+  tm = first + r % rows;
+  tn = r / rows;
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int MF, int AMODE, bool NORM, int EPI,
@@ -279,7 +296,8 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int gn = gridDim.x;
   const int tile = xcd_remap(blockIdx.y * gn + blockIdx.x, gn * gridDim.y);
-  const int tm_idx = tile / gn, tn_idx = tile - (tile / gn) * gn;
+  int tm_idx, tn_idx;
+  tile_coords(tile, gridDim.y, gn, tm_idx, tn_idx);
   const int m0 = tm_idx * BM, n0 = tn_idx * BN;
   const int kt_begin = 0;
   const int kt_end = (p.K + BK - 1) / BK;
@@ -467,7 +485,8 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
   const int wm = wave >> 1, wn = wave & 1;
   const int gn = gridDim.x;
   const int tile = xcd_remap(blockIdx.y * gn + blockIdx.x, gn * gridDim.y);
-  const int tm_idx = tile / gn, tn_idx = tile - tm_idx * gn;
+  int tm_idx, tn_idx;
+  tile_coords(tile, gridDim.y, gn, tm_idx, tn_idx);
   const int m0 = tm_idx * PBM, n0 = tn_idx * PBN;
   const int nk = (p.K + PBK - 1) / PBK;
 
@@ -697,7 +716,8 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   const int wm = wave >> 1, wn = wave & 1;
   const int gn = gridDim.x;
   const int tile = xcd_remap(blockIdx.y * gn + blockIdx.x, gn * gridDim.y);
-  const int tm_idx = tile / gn, tn_idx = tile - tm_idx * gn;
+  int tm_idx, tn_idx;
+  tile_coords(tile, gridDim.y, gn, tm_idx, tn_idx);
   const int m0 = tm_idx * WBM, n0 = tn_idx * WBN;
   const int nk = p.K / WBK;  // K % (4 * WBK) == 0 (checked by the launcher)
 
