@@ -7,31 +7,17 @@
 // scores and softmax statistics in fp32, probabilities rounded to bf16 before
 // the P.V product, fp32 accumulation, bf16 output.
 //
-// Work decomposition: one workgroup = 64 query rows of one query head
-// (4 waves x 16 rows); the loop runs over blocks of 64 keys of the head's KV
-// group (h * hkv / hq), staged in LDS and shared by the 4 waves.
-//
-// MFMA layout trick: every product is computed transposed,
-//   S^T[key, q] = K . Q^T         (A = K tile from LDS, B = the wave's Q rows)
-//   O^T[d, q]  += V^T . P^T       (A = V^T tile from LDS, B = P^T from registers)
-// With v_mfma_f32_16x16x32_bf16 the accumulator of lane l holds 4 consecutive
-// rows of column (l & 15); transposing puts the QUERY on the column, so each
-// lane owns one query's scores, running max, running sum and output -- the
-// online-softmax rescale is lane-local and the row reductions are two
-// cross-lane shuffles (lanes l, l^16, l^32).  The S^T accumulators of two
-// consecutive 16-key subtiles are exactly the B operand P^T of the next MFMA
-// (keys {4g..4g+3} u {16+4g..16+4g+3} in k-slots 8g..8g+7); the V^T operand is
-// read with the same key permutation, so no shuffles are needed between the
-// two products.
+// Work decomposition: one workgroup = 128 query rows of one query head
+// (4 waves x 32 rows); K/V blocks of 64 keys stream through a 3-stage LDS
+// ring (see attention_kernel).
 #include "svla_common.h"
 
 namespace {
 
 constexpr int D = 64;
-constexpr int BQ = 64;     // query rows per workgroup
-constexpr int BKEY = 64;   // keys per LDS block
-constexpr int KS = D + 8;  // padded LDS row (elements) for the K tile
-constexpr int VS = BKEY + 8;
+constexpr int BKEY = 64;   // keys per LDS stage
+constexpr int QW = 32;     // query rows per wave (two 16-column MFMA tiles)
+constexpr int BQ = 4 * QW; // query rows per workgroup
 
 struct AttnArgs {
   const bf16* q; long ldq, q_bs;
@@ -43,134 +29,268 @@ struct AttnArgs {
   int mask_kind, prefix_len;
 };
 
-__device__ __forceinline__ bool masked(int kind, int qi, int kj, int prefix_len) {
-  if (kind == SVLA_MASK_CAUSAL) return kj > qi;
-  if (kind == SVLA_MASK_PREFIX_LM) return kj > qi && kj >= prefix_len;
-  return false;
+// Keys a query row may see, as one bound: key j is visible to row i iff
+// j < key_limit(i).  causal: j <= i; prefix-LM: j <= i or j < prefix_len
+// (the bidirectional prefix block); none: every key.  Always also j < sk.
+__device__ __forceinline__ int key_limit(int kind, int qi, int sk, int prefix_len) {
+  const int pre = kind == SVLA_MASK_NONE ? sk : (kind == SVLA_MASK_PREFIX_LM ? prefix_len : 0);
+  return min(sk, max(qi + 1, pre));
 }
 
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs p) {
-  __shared__ __attribute__((aligned(16))) bf16 sK[BKEY * KS];
-  __shared__ __attribute__((aligned(16))) bf16 sVt[D * VS];
+// LDS stage = K tile [64 keys][64 d] + V tile [64 keys][64 d], both row-major
+// with the 16-byte chunk c of key row r stored in slot c ^ (r & 7), so that
+// both the K fragment reads (16 keys x one chunk) and the V transpose reads
+// (4 keys x 4 chunks per 16 lanes) spread over the banks.
+__device__ __forceinline__ int kv_off(int key, int d) {  // element offset, d % 4 == 0
+  return key * D + ((((d >> 3) ^ key) & 7) << 3) + (d & 7);
+}
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
+
+// Reductions over lanes l ^ 16 and l ^ 32 with the gfx950 row-swap VALU ops
+// (v_permlane16_swap / v_permlane32_swap): called with both operands = x,
+// every lane ends up holding {x[l], x[l ^ 16]} (resp. l ^ 32) in some order.
+// No LDS round trip, unlike a ds_bpermute shuffle.
+__device__ __forceinline__ float max_xor16(float x) {
+  const u32x2_t r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const u32x2_t r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const u32x2_t r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const u32x2_t r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+typedef __attribute__((address_space(3))) v4i16* lds_v4i16_ptr;
+
+// V^T operand of O^T += V^T . P^T via the LDS transpose read: within each
+// 16-lane group, lane j receives element (j & 3) of the 8-byte chunks of
+// lanes (j >> 2) + 4t, t = 0..3.  Lane i = 4t + r of the group points at
+// V[kbase + t][dbase + 4r], so lane j gets V[kbase + t][dbase + j], t = 0..3:
+// 4 consecutive keys of head dim (dbase + j).
+__device__ __forceinline__ v4i16 v_tr_read(const bf16* sv, int kbase, int dbase, int i) {
+  const int t = i >> 2, r = i & 3;
+  const bf16* p = sv + kv_off(kbase + t, dbase + 4 * r);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16_ptr)(p));
+}
+
+// One workgroup = 128 query rows of one query head (4 waves x 32 rows); the
+// loop streams blocks of 64 keys of the head's KV group (h * hkv / hq)
+// through a 3-stage ring of LDS buffers filled by global_load_lds.
+//
+// Products are computed transposed,
+//   S^T[key, q] = K . Q^T         (A = K fragment from LDS, B = the wave's Q)
+//   O^T[d, q]  += V^T . P^T       (A = V^T via transpose read, B = P^T)
+// so that with v_mfma_f32_16x16x32_bf16 each lane owns one query column: the
+// online-softmax statistics are lane-local and the row reductions are two
+// shuffles (lanes l, l^16, l^32).  The S^T accumulators of two consecutive
+// 16-key subtiles are exactly the B operand P^T of the next MFMA (keys
+// {4g..4g+3} u {16+4g..16+4g+3} in k-slots 8g..8g+7, g = lane / 16); the V^T
+// operand is read with the same key order.
+// FULL: no mask and sk % 64 == 0, so no per-score checks at all.
+template <bool FULL>
+__global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
+  __shared__ __attribute__((aligned(1024))) bf16 sK0[BKEY * D], sK1[BKEY * D], sK2[BKEY * D];
+  __shared__ __attribute__((aligned(1024))) bf16 sV0[BKEY * D], sV1[BKEY * D], sV2[BKEY * D];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = blockIdx.y, b = blockIdx.z;
-  const int g = h * p.hkv / p.hq;
+  const int kvh = h * p.hkv / p.hq;
   const int q0 = blockIdx.x * BQ;
-  const int qi = q0 + wave * 16 + (lane & 15);  // this lane's query row
-  const int grp = lane >> 4;                     // 0..3
+  const int grp = lane >> 4, col = lane & 15;
+  const int qw = q0 + wave * QW;                 // first query row of this wave
 
   const bf16* qb = p.q + b * p.q_bs + h * D;
-  const bf16* kb = p.k + b * p.k_bs + g * D;
-  const bf16* vb = p.v + b * p.v_bs + g * D;
-
-  // B operand of S^T: Q[qi][ks*32 + 8*grp .. +7]
-  bf16x8 qf[2];
-#pragma unroll
-  for (int ks = 0; ks < 2; ++ks)
-    qf[ks] = qi < p.sq ? ld8(qb + (long)qi * p.ldq + ks * 32 + grp * 8) : bf16x8{};
+  const bf16* kb = p.k + b * p.k_bs + kvh * D;
+  const bf16* vb = p.v + b * p.v_bs + kvh * D;
 
   // last key any row of this workgroup may see
   int kend = p.sk;
-  if (p.mask_kind != SVLA_MASK_NONE) {
+  if (!FULL && p.mask_kind != SVLA_MASK_NONE) {
     const int qmax = min(p.sq, q0 + BQ) - 1;
     int lim = qmax + 1;
     if (p.mask_kind == SVLA_MASK_PREFIX_LM) lim = max(lim, p.prefix_len);
     kend = min(kend, lim);
   }
+  const int nb = (kend + BKEY - 1) / BKEY;
 
-  f32x4 o[4];
+  // DMA: each stage is 8 + 8 instructions of 1 KB (8 key rows each); wave w
+  // issues K and V rows 16w .. 16w+15.  Lane -> key row lane / 8, LDS slot
+  // lane % 8 holding logical chunk slot ^ (row & 7).  Rows past sk are
+  // clamped (masked or never used).
+  long koff[2], voff[2];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) o[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
-
-  for (int k0 = 0; k0 < kend; k0 += BKEY) {
-    // stage K [64 keys][64 d] and V^T [64 d][64 keys]
+  for (int j = 0; j < 2; ++j) {
+    const int key = (wave * 2 + j) * 8 + (lane >> 3);
+    const int c = (lane & 7) ^ (key & 7);
+    koff[j] = (long)key * p.ldk + c * 8;
+    voff[j] = (long)key * p.ldv + c * 8;
+  }
+  auto issue = [&](auto SI, int blk) {
+    constexpr int S = decltype(SI)::value;
+    bf16* sk = S == 0 ? sK0 : S == 1 ? sK1 : sK2;
+    bf16* sv = S == 0 ? sV0 : S == 1 ? sV1 : sV2;
+    blk = min(blk, nb - 1);  // past the end: reload the last block (never read)
+    const int k0 = blk * BKEY;
+    const int rows_left = p.sk - 1 - k0;  // clamp rows into the tensor
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + i * 256;
-      const int key = c >> 3, dc = (c & 7) * 8;
-      const int kj = k0 + key;
-      bf16x8 kv = kj < p.sk ? ld8(kb + (long)kj * p.ldk + dc) : bf16x8{};
-      bf16x8 vv = kj < p.sk ? ld8(vb + (long)kj * p.ldv + dc) : bf16x8{};
-      *reinterpret_cast<bf16x8*>(&sK[key * KS + dc]) = kv;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sVt[(dc + j) * VS + key] = vv[j];
+    for (int j = 0; j < 2; ++j) {
+      const int key = (wave * 2 + j) * 8 + (lane >> 3);
+      const long adj = key > rows_left ? (long)(rows_left - key) : 0;
+      const bf16* gk = kb + (long)k0 * p.ldk + koff[j] + adj * p.ldk;
+      const bf16* gv = vb + (long)k0 * p.ldv + voff[j] + adj * p.ldv;
+      __builtin_amdgcn_global_load_lds((void*)gk, (lds_ptr_t)(sk + (wave * 2 + j) * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((void*)gv, (lds_ptr_t)(sv + (wave * 2 + j) * 512), 16, 0, 0);
     }
-    __syncthreads();
+  };
 
-    // S^T for 4 subtiles of 16 keys
-    float s[4][4];
+  // Q fragments (B operand of S^T): rows qw + 16 qt + col, d = 32 ks + 8 grp.
+  // Rows past sq are clamped (their outputs are never stored); loading
+  // without a branch keeps the loads in flight across the DMA prologue.
+  bf16x8 qf[2][2];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qi = min(qw + qt * 16 + col, p.sq - 1);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) qf[qt][ks] = ld8(qb + (long)qi * p.ldq + ks * 32 + grp * 8);
+  }
+
+  f32x4 o[2][4];
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) o[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int klim[2];  // per query tile: this lane's query sees keys < klim
+#pragma unroll
+  for (int qt = 0; qt < 2; ++qt)
+    klim[qt] = key_limit(p.mask_kind, qw + qt * 16 + col, p.sk, p.prefix_len);
+  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  const float c = p.scale_log2;
+
+  auto compute = [&](auto SI, int blk) {
+    constexpr int S = decltype(SI)::value;
+    const bf16* sk = S == 0 ? sK0 : S == 1 ? sK1 : sK2;
+    const bf16* sv = S == 0 ? sV0 : S == 1 ? sV1 : sV2;
+    const int k0 = blk * BKEY;
+    // S^T: 4 key subtiles x 2 query tiles, K fragments shared by both
+    f32x4 sacc[4][2];
 #pragma unroll
     for (int ts = 0; ts < 4; ++ts) {
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+      bf16x8 kf[2];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const bf16x8 kf =
-            *reinterpret_cast<const bf16x8*>(&sK[(ts * 16 + (lane & 15)) * KS + ks * 32 + grp * 8]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], acc, 0, 0, 0);
-      }
+      for (int ks = 0; ks < 2; ++ks)
+        kf[ks] = *reinterpret_cast<const bf16x8*>(&sk[kv_off(ts * 16 + col, ks * 32 + grp * 8)]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int kj = k0 + ts * 16 + grp * 4 + i;
-        const bool dead = kj >= p.sk || masked(p.mask_kind, qi, kj, p.prefix_len);
-        s[ts][i] = dead ? -INFINITY : acc[i] * p.scale_log2;
+      for (int qt = 0; qt < 2; ++qt) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+          a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[qt][ks], a, 0, 0, 0);
+        sacc[ts][qt] = a;
       }
     }
-    // row max over this block: 16 local values, then lanes l, l^16, l^32, l^48
-    float mx = s[0][0];
+    // online softmax per query tile (lane-local statistics)
+    bf16x8 pf[2][2];
 #pragma unroll
-    for (int ts = 0; ts < 4; ++ts)
+    for (int qt = 0; qt < 2; ++qt) {
+      if constexpr (!FULL) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[ts][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;  // fully-masked-so-far guard
-    const float alpha = exp2f(m_run - m_use);
-    float psum = 0.f;
-    bf16x8 pf[2];
+        for (int ts = 0; ts < 4; ++ts)
 #pragma unroll
-    for (int ts = 0; ts < 4; ++ts)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float e = exp2f(s[ts][i] - m_use);
-        psum += e;
-        pf[ts >> 1][(ts & 1) * 4 + i] = f2bf(e);
+          for (int i = 0; i < 4; ++i) {
+            const int kj = k0 + ts * 16 + grp * 4 + i;
+            sacc[ts][qt][i] = kj < klim[qt] ? sacc[ts][qt][i] : -INFINITY;
+          }
       }
-    psum += __shfl_xor(psum, 16, 64);
-    psum += __shfl_xor(psum, 32, 64);
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+      float mx = sacc[0][qt][0];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) o[t] *= alpha;
-
-    // O^T[d, q] += V^T[d, keys] . P^T[keys, q]
+      for (int ts = 0; ts < 4; ++ts)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[ts][qt][i]);
+      mx = max_xor32(max_xor16(mx));
+      const float m_new = fmaxf(m_run[qt], mx);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // fully-masked-so-far guard
+      const float mc = m_use * c;
+      const float alpha = __builtin_amdgcn_exp2f(m_run[qt] * c - mc);
+      float psum = 0.f;
+#pragma unroll
+      for (int ts = 0; ts < 4; ++ts)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[ts][qt][i], c, -mc));
+          psum += e;
+          pf[qt][ts >> 1][(ts & 1) * 4 + i] = f2bf(e);
+        }
+      psum = sum_xor32(sum_xor16(psum));
+      l_run[qt] = l_run[qt] * alpha + psum;
+      m_run[qt] = m_new;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) o[qt][t] *= alpha;
+    }
+    // O^T[d, q] += V^T[d, keys] . P^T[keys, q]; V^T fragments shared by both query tiles
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
       for (int td = 0; td < 4; ++td) {
-        const bf16* vrow = &sVt[(td * 16 + (lane & 15)) * VS + kk * 32 + grp * 4];
-        const bf16x4 lo = *reinterpret_cast<const bf16x4*>(vrow);
-        const bf16x4 hi = *reinterpret_cast<const bf16x4*>(vrow + 16);
-        bf16x8 vf;
-        vf[0] = lo[0]; vf[1] = lo[1]; vf[2] = lo[2]; vf[3] = lo[3];
-        vf[4] = hi[0]; vf[5] = hi[1]; vf[6] = hi[2]; vf[7] = hi[3];
-        o[td] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[kk], o[td], 0, 0, 0);
+        const v4i16 lo = v_tr_read(sv, kk * 32 + 4 * grp, td * 16, col);
+        const v4i16 hi = v_tr_read(sv, kk * 32 + 16 + 4 * grp, td * 16, col);
+        const v4i16 w8[2] = {lo, hi};
+        bf16x8 vf = *reinterpret_cast<const bf16x8*>(w8);
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+          o[qt][td] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qt][kk], o[qt][td], 0, 0, 0);
       }
     }
-    __syncthreads();
-  }
+  };
 
-  if (qi >= p.sq) return;
-  const float inv = l_run > 0.f ? 1.0f / l_run : 0.f;
-  bf16* orow = p.o + b * p.o_bs + (long)qi * p.ldo + h * D;
+  // s_waitcnt vmcnt(N): a stage is 4 DMA instructions per wave; the next
+  // stage stays in flight (gfx9 encoding, expcnt / lgkmcnt unconstrained)
+  constexpr int kWaitOne = 0xF70 | 4;
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  // Q is needed by every block: wait for it here, before the DMA prologue,
+  // so the compiler has no pending load to drain at the loop entry
+  __builtin_amdgcn_s_waitcnt(0xF70);
+  issue(I0{}, 0);
+  issue(I1{}, 1);
+  for (int blk = 0; blk < nb; blk += 3) {
+    __builtin_amdgcn_s_waitcnt(kWaitOne);
+    __builtin_amdgcn_s_barrier();
+    issue(I2{}, blk + 2);
+    compute(I0{}, blk);
+    __builtin_amdgcn_s_waitcnt(kWaitOne);
+    __builtin_amdgcn_s_barrier();
+    issue(I0{}, blk + 3);
+    if (blk + 1 < nb) compute(I1{}, blk + 1);
+    __builtin_amdgcn_s_waitcnt(kWaitOne);
+    __builtin_amdgcn_s_barrier();
+    issue(I1{}, blk + 4);
+    if (blk + 2 < nb) compute(I2{}, blk + 2);
+  }
+  // drain the trailing (never read) DMA before the workgroup exits
+  __builtin_amdgcn_s_waitcnt(0);
+
 #pragma unroll
-  for (int td = 0; td < 4; ++td) {
-    bf16x4 r;
+  for (int qt = 0; qt < 2; ++qt) {
+    const int qi = qw + qt * 16 + col;
+    if (qi >= p.sq) continue;
+    const float inv = l_run[qt] > 0.f ? 1.0f / l_run[qt] : 0.f;
+    bf16* orow = p.o + b * p.o_bs + (long)qi * p.ldo + h * D;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = f2bf(o[td][i] * inv);
-    *reinterpret_cast<bf16x4*>(orow + td * 16 + grp * 4) = r;
+    for (int td = 0; td < 4; ++td) {
+      bf16x4 r;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = f2bf(o[qt][td][i] * inv);
+      *reinterpret_cast<bf16x4*>(orow + td * 16 + grp * 4) = r;
+    }
   }
 }
 
@@ -200,7 +320,10 @@ extern "C" int svla_attention_bf16(const void* q, int ldq, long q_bs, const void
   p.mask_kind = mask_kind;
   p.prefix_len = prefix_len;
   dim3 grid((sq + BQ - 1) / BQ, hq, batch);
-  hipLaunchKernelGGL(attention_kernel, grid, dim3(256), 0, (hipStream_t)stream, p);
+  if (mask_kind == SVLA_MASK_NONE && sk % BKEY == 0)
+    hipLaunchKernelGGL(attention_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, p);
+  else
+    hipLaunchKernelGGL(attention_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, p);
   SVLA_CHECK_LAUNCH();
   return SVLA_OK;
 }
