@@ -92,8 +92,8 @@ int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void*
 /* Tuning hook: force the GEMM tile configuration for every later call
  * (0: 256x256/32x32-MFMA, 1: 128x128/32x32, 2: 64x128/16x16, 3: 64x64/16x16,
  * 4: skinny 64x64, 5: skinny 64x32, 6: 128x128/16x16, 7: 128x128 4-stage LDS-DMA
- * pipeline, 8: 256x256 4-stage LDS-DMA pipeline with 128x128 wave tiles), or -1
- * for the automatic
+ * pipeline, 8: 256x256 4-stage LDS-DMA pipeline with 128x128 wave tiles, 9: 64x64
+ * 4-stage LDS-DMA pipeline), or -1 for the automatic
  * shape-based choice (default).  Process-wide; not thread-safe. */
 int svla_gemm_set_tile(int tile);
 

@@ -9,6 +9,11 @@ Per decoder layer (vla/text_encoder_bf16.py:480-595 -> 5 launches):
   [RMSNorm -> QKV GEMM -> RoPE] -> fused GQA attention -> [O GEMM + residual]
   -> [RMSNorm -> gate|up GEMM -> SiLU*up] -> [down GEMM + residual]
 (brackets = one kernel: the norms run in the GEMM's A-operand prologue).
+That fusion pays only for few rows (M <= FUSED_NORM_MAX_ROWS, the skinny GEMM
+path, where a launch costs more than the norm); above it the row statistics
+and per-element scaling inside the GEMM cost more than a standalone RMSNorm
+pass (measured on MI355X: prefix QKV at batch 32 116 us fused vs 6 + 50 us
+split), so the norm runs as its own kernel (7 launches per layer).
 """
 
 from __future__ import annotations
@@ -111,6 +116,18 @@ class Buffers:
 
 
 # ----------------------------------------------------------------- layers ---
+# the GEMM runs its skinny kernel up to 256 rows; fuse the RMSNorm there only
+FUSED_NORM_MAX_ROWS = 256
+
+
+def _normed(x, w, eps, M, bufs, name):
+    """(A operand, norm argument) for a GEMM that consumes RMSNorm(x): fused
+    into the GEMM for few rows, else a standalone RMSNorm into a buffer."""
+    if M <= FUSED_NORM_MAX_ROWS:
+        return x, (w, eps)
+    return ops.rmsnorm(x, w, eps, out=bufs.get(name, M, x.shape[1])), None
+
+
 def decoder_layer(x, P, cfg: DecoderConfig, B, L, rope: Rope, mask="causal", prefix_len=0,
                   bufs: Optional[Buffers] = None, qkv_out=None, mid_out=None):
     """One SmolLM2-style block on ``x [B*L, H]`` **in place**; returns the
@@ -122,8 +139,8 @@ def decoder_layer(x, P, cfg: DecoderConfig, B, L, rope: Rope, mask="causal", pre
     qd, kvd = cfg.q_dim, cfg.kv_dim
     eps = resolve_eps(cfg.rms_eps)
     qkv = qkv_out if qkv_out is not None else bufs.get("qkv", M, qd + 2 * kvd)
-    ops.linear_rope(x, P["wqkv"], qd + kvd, L, rope.cos, rope.sin, out=qkv,
-                    norm=(P["n1"], eps))
+    a, nrm = _normed(x, P["n1"], eps, M, bufs, "xn")
+    ops.linear_rope(a, P["wqkv"], qd + kvd, L, rope.cos, rope.sin, out=qkv, norm=nrm)
     q3 = qkv.view(B, L, -1)
     attn = bufs.get("attn", M, qd)
     ops.attention(q3[:, :, :qd], q3[:, :, qd:qd + kvd], q3[:, :, qd + kvd:],
@@ -136,8 +153,8 @@ def decoder_layer(x, P, cfg: DecoderConfig, B, L, rope: Rope, mask="causal", pre
 
 
 def _mlp(x, P, cfg, M, eps, bufs):
-    act = ops.linear_silu_mul(x, P["wgu"], out=bufs.get("mlp", M, cfg.inter),
-                              norm=(P["n2"], eps))
+    a, nrm = _normed(x, P["n2"], eps, M, bufs, "xn")
+    act = ops.linear_silu_mul(a, P["wgu"], out=bufs.get("mlp", M, cfg.inter), norm=nrm)
     ops.linear(act, P["wd"], res=x, out=x)
 
 
@@ -158,8 +175,9 @@ def cross_layer(x, ck, cv, P, cfg: DecoderConfig, B, L, Lc, rope: Rope,
     M = B * L
     qd = cfg.q_dim
     eps = resolve_eps(cfg.rms_eps)
-    q = ops.linear_rope(x, P["wq"], qd, L, rope.cos, rope.sin, out=bufs.get("q", M, qd),
-                        norm=(P["n1"], eps))
+    a, nrm = _normed(x, P["n1"], eps, M, bufs, "xn")
+    q = ops.linear_rope(a, P["wq"], qd, L, rope.cos, rope.sin, out=bufs.get("q", M, qd),
+                        norm=nrm)
     attn = bufs.get("attn", M, qd)
     ops.attention(q.view(B, L, qd), ck.view(B, Lc, -1), cv.view(B, Lc, -1), attn.view(B, L, qd),
                   cfg.n_q_heads, cfg.n_kv_heads, "none", 0)
