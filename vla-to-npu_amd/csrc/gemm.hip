@@ -109,105 +109,133 @@ __device__ __forceinline__ void load_bf16x4(const bf16* src, float v[4]) {
 }
 
 // ---- epilogues: 4 consecutive (packed) columns of one row ------------------
-// Values already include alpha.
-template <int ACT>
-__device__ __forceinline__ void epi_store(const GemmArgs& p, int m, int n, float v[4]) {
-  if (p.bias) {
-    float b[4];
-    load_bf16x4(p.bias + n, b);
+// Split in two so that a kernel issues the loads of a whole column tile's
+// output groups before its first store: epi_load_groups reads the optional
+// operands (bias, residual, position addend, RoPE tables, Euler state) of G
+// groups -- one uniform branch region per optional operand, holding that
+// operand's loads for all G groups, so they are in flight together -- and
+// epi_apply blends them in and stores one group.  (A residual may alias the
+// output, so a load issued after an earlier group's store could not be
+// hoisted above it; and a region per group and operand would end each one
+// with a full vmcnt(0) drain: either way the loads would run one by one.)
+struct EpiIn {
+  f32x4 u, w;      // fp32 bias | RoPE cos, sin | Euler x
+  bf16x4 b, r, a;  // bf16 bias, residual, row-periodic addend
+};
+
+// m, n: each group's (row, first column), clamped into range by the caller
+template <int EPI, int G>
+__device__ __forceinline__ void epi_load_groups(const GemmArgs& p, const int (&m)[G],
+                                                const int (&n)[G], EpiIn (&e)[G]) {
+  if constexpr (EPI == EPI_STORE) {
+    if (p.bias) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] += b[i];
-  }
-  if (p.bias_f32) {
+      for (int g = 0; g < G; ++g) e[g].b = *reinterpret_cast<const bf16x4*>(p.bias + n[g]);
+    }
+    if (p.bias_f32) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] += p.bias_f32[n + i];
-  }
-  if (p.out_f32) {
-    float* dst = reinterpret_cast<float*>(p.c) + crow(p, m) * p.ldc + n;
-    *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
-    return;
-  }
+      for (int g = 0; g < G; ++g) e[g].u = *reinterpret_cast<const f32x4*>(p.bias_f32 + n[g]);
+    }
+    if (p.res) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) v[i] = rbf(v[i]);
-  if constexpr (ACT != SVLA_ACT_NONE) {
+      for (int g = 0; g < G; ++g)
+        e[g].r = *reinterpret_cast<const bf16x4*>(p.res + (long)m[g] * p.ldr + n[g]);
+    }
+    if (p.rowadd) {  // patch embedding's position table
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = rbf(apply_act<ACT>(v[i]));
-  }
-  if (p.rowadd) {
-    float r[4];
-    load_bf16x4(p.rowadd + (long)(m % p.rowadd_period) * p.N + n, r);
+      for (int g = 0; g < G; ++g)
+        e[g].a = *reinterpret_cast<const bf16x4*>(p.rowadd + (long)(m[g] % p.rowadd_period) * p.N + n[g]);
+    }
+  } else if constexpr (EPI == EPI_ROPE) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = rbf(v[i] + r[i]);
-  }
-  if (p.res) {
-    float r[4];
-    load_bf16x4(p.res + (long)m * p.ldr + n, r);
+    for (int g = 0; g < G; ++g) {
+      const int pos = m[g] % p.rope_period;
+      const int d = n[g] & 63;  // < 32: n is in the first half of its 64-column block
+      e[g].u = *reinterpret_cast<const f32x4*>(p.rope_cos + pos * 32 + d);
+      e[g].w = *reinterpret_cast<const f32x4*>(p.rope_sin + pos * 32 + d);
+    }
+  } else if constexpr (EPI == EPI_EULER) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = rbf(v[i] + r[i]);
+    for (int g = 0; g < G; ++g)
+      e[g].u = *reinterpret_cast<const f32x4*>(p.x_f32 + (long)m[g] * p.ldx + n[g]);
   }
-  store_bf16x4(reinterpret_cast<bf16*>(p.c) + crow(p, m) * p.ldc + n, v);
 }
 
-// RoPE pair: x1 at columns n1..n1+3 (head dims d..d+3 < 32), x2 at n1+32.
-// Mirrors apply_rope on the bf16 projection (vla/text_encoder_bf16.py:92-104):
-// out1 = x1*cos - x2*sin, out2 = x2*cos + x1*sin in fp32, then bf16.
-__device__ __forceinline__ void epi_rope(const GemmArgs& p, int m, int n1, float x1[4],
-                                         float x2[4]) {
-  bf16* c = reinterpret_cast<bf16*>(p.c) + crow(p, m) * p.ldc;
+// v (x1) = this group's 4 accumulators (times alpha); x2 = the paired group
+// 32 columns on (RoPE / SiLU epilogues only).
+template <int EPI, int ACT>
+__device__ __forceinline__ void epi_apply(const GemmArgs& p, int m, int n, float* v, float* x2,
+                                          const EpiIn& e) {
+  if constexpr (EPI == EPI_STORE) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) { x1[i] = rbf(x1[i]); x2[i] = rbf(x2[i]); }
-  if (n1 < p.rope_cols) {
-    const int pos = m % p.rope_period;
-    const int d = n1 & 63;
-    const float* ct = p.rope_cos + pos * 32 + d;
-    const float* st = p.rope_sin + pos * 32 + d;
+    for (int i = 0; i < 4; ++i) {
+      if (p.bias) v[i] += bf2f(e.b[i]);
+      if (p.bias_f32) v[i] += e.u[i];
+    }
+    if (p.out_f32) {
+      float* dst = reinterpret_cast<float*>(p.c) + crow(p, m) * p.ldc + n;
+      *reinterpret_cast<f32x4*>(dst) = f32x4{v[0], v[1], v[2], v[3]};
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = rbf(v[i]);
+    if constexpr (ACT != SVLA_ACT_NONE) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = rbf(apply_act<ACT>(v[i]));
+    }
+    if (p.rowadd) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = rbf(v[i] + bf2f(e.a[i]));
+    }
+    if (p.res) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = rbf(v[i] + bf2f(e.r[i]));
+    }
+    store_bf16x4(reinterpret_cast<bf16*>(p.c) + crow(p, m) * p.ldc + n, v);
+  } else if constexpr (EPI == EPI_ROPE) {
+    // mirrors apply_rope on the bf16 projection (vla/text_encoder_bf16.py:92-104):
+    // out1 = x1*cos - x2*sin, out2 = x2*cos + x1*sin in fp32, then bf16;
+    // columns past rope_cols (V) are stored unrotated
+    bf16* c = reinterpret_cast<bf16*>(p.c) + crow(p, m) * p.ldc;
+    const bool rot = n < p.rope_cols;
     float o1[4], o2[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float cs = ct[i], sn = st[i];
-      o1[i] = __fsub_rn(__fmul_rn(x1[i], cs), __fmul_rn(x2[i], sn));
-      o2[i] = __fadd_rn(__fmul_rn(x2[i], cs), __fmul_rn(x1[i], sn));
+      const float x1 = rbf(v[i]), y2 = rbf(x2[i]);
+      const float r1 = __fsub_rn(__fmul_rn(x1, e.u[i]), __fmul_rn(y2, e.w[i]));
+      const float r2 = __fadd_rn(__fmul_rn(y2, e.u[i]), __fmul_rn(x1, e.w[i]));
+      o1[i] = rot ? r1 : x1;
+      o2[i] = rot ? r2 : y2;
     }
-    store_bf16x4(c + n1, o1);
-    store_bf16x4(c + n1 + 32, o2);
+    store_bf16x4(c + n, o1);
+    store_bf16x4(c + n + 32, o2);
+  } else if constexpr (EPI == EPI_SILU) {
+    // gate at packed column n (first half of a 64-block), up at n + 32; output
+    // column (n / 64) * 32 + n % 64; out = bf16(bf16(silu(bf16(g))) * bf16(u))
+    // (nn.SiLU on the bf16 gate projection, then the bf16 hadamard product,
+    // vla/text_encoder_bf16.py:130-131)
+    float o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[i] = rbf(silu_f(rbf(v[i]))) * rbf(x2[i]);
+    const int nout = (n >> 6) * 32 + (n & 63);
+    store_bf16x4(reinterpret_cast<bf16*>(p.c) + crow(p, m) * p.ldc + nout, o);
   } else {
-    store_bf16x4(c + n1, x1);
-    store_bf16x4(c + n1 + 32, x2);
-  }
-}
-
-// Gated MLP pair: gate at packed column ng (first half of a 64-block), up at
-// ng + 32; output column (ng / 64) * 32 + ng % 64.
-// out = bf16(bf16(silu(bf16(g))) * bf16(u))  (nn.SiLU on the bf16 gate
-// projection, then the bf16 hadamard product, vla/text_encoder_bf16.py:130-131)
-__device__ __forceinline__ void epi_silu(const GemmArgs& p, int m, int ng, float g[4],
-                                         float u[4]) {
-  float o[4];
+    // Euler step x <- x + dt * bf16(v) in fp32 (+ optional bf16 copy of x)
+    float o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = rbf(silu_f(rbf(g[i]))) * rbf(u[i]);
-  const int nout = (ng >> 6) * 32 + (ng & 63);
-  store_bf16x4(reinterpret_cast<bf16*>(p.c) + crow(p, m) * p.ldc + nout, o);
-}
-
-// Euler step x <- x + dt * bf16(v) in fp32 (+ optional bf16 copy of x).
-__device__ __forceinline__ void epi_euler(const GemmArgs& p, int m, int n, float v[4]) {
-  float* x = p.x_f32 + (long)m * p.ldx + n;
-  float o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o[i] = __fadd_rn(x[i], __fmul_rn(p.dt, rbf(v[i])));
-    x[i] = o[i];
+    for (int i = 0; i < 4; ++i) o[i] = __fadd_rn(e.u[i], __fmul_rn(p.dt, rbf(v[i])));
+    *reinterpret_cast<f32x4*>(p.x_f32 + (long)m * p.ldx + n) = f32x4{o[0], o[1], o[2], o[3]};
+    if (p.x_bf16) store_bf16x4(p.x_bf16 + (long)m * p.ldxb + n, o);
   }
-  if (p.x_bf16) store_bf16x4(p.x_bf16 + (long)m * p.ldxb + n, o);
 }
 
 // ---- A operand gather -------------------------------------------------------
+// Address of A[m][k .. k+7] for an in-range (m, k); no bounds checks, so
+// callers can clamp (m, k) and issue the load without a branch.
 template <int AMODE>
-__device__ __forceinline__ bf16x8 load_a(const GemmArgs& p, int m, int k) {
-  if (m >= p.M || k >= p.K) return bf16x8{};
-  const bf16* src;
+__device__ __forceinline__ const bf16* a_ptr(const GemmArgs& p, int m, int k) {
   if constexpr (AMODE == A_DENSE) {
-    src = p.a + (long)m * p.lda + k;
+    return p.a + (long)m * p.lda + k;
   } else if constexpr (AMODE == A_PSHUF) {
     // out[i][t*(s*E) + u*E + c] = x[(s*(i/gs) + t)*grid + s*(i%gs) + u][c]
     // with gs = grid/s (the reshape/transpose chain of vla/vla.py:435)
@@ -220,7 +248,7 @@ __device__ __forceinline__ bf16x8 load_a(const GemmArgs& p, int m, int k) {
     const int t = k / sE, rem = k - t * sE;
     const int u = rem / E, c = rem - u * E;
     const long tok = (long)(s * hp + t) * grid + s * wp + u;
-    src = p.a + ((long)img * grid * grid + tok) * E + c;
+    return p.a + ((long)img * grid * grid + tok) * E + c;
   } else {
     // im2col of Conv2d(k = stride = P): row = img*G*G + pr*G + pc,
     // col = ch*P*P + ky*P + kx (the conv weight's [E, C, P, P] flattening)
@@ -231,9 +259,14 @@ __device__ __forceinline__ bf16x8 load_a(const GemmArgs& p, int m, int k) {
     const int P2 = P * P;
     const int ch = k / P2, r = k - ch * P2;
     const int ky = r / P, kx = r - ky * P;
-    src = p.a + (((long)img * p.p_chans + ch) * H + pr * P + ky) * H + pc * P + kx;
+    return p.a + (((long)img * p.p_chans + ch) * H + pr * P + ky) * H + pc * P + kx;
   }
-  return ld8(src);
+}
+
+template <int AMODE>
+__device__ __forceinline__ bf16x8 load_a(const GemmArgs& p, int m, int k) {
+  if (m >= p.M || k >= p.K) return bf16x8{};
+  return ld8(a_ptr<AMODE>(p, m, k));
 }
 
 constexpr int BK = 64;
@@ -334,30 +367,34 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
 
   bf16x8 ra[A_CH], rb[B_CH];
   bf16x8 rw;  // norm gain for this thread's A k-chunk (the same for all its chunks)
+  bool kin = true;  // this thread's k-chunk lies inside K (its column is the same in A and B)
 
-  auto gload = [&](int kt) {
+  // Every load is issued unconditionally from a clamped address (rows past
+  // M / N only feed outputs that are never stored); chunks past K are zeroed
+  // when they are written to LDS.  Loads under a branch would each end their
+  // own region with a full vmcnt(0) drain and serialise the prefetch.
+  auto gload = [&](int kt) __attribute__((always_inline)) {
     const int kb = kt * BK;
+    const int k = kb + (tid & 7) * 8;  // c & 7 == tid & 7 for every chunk c
+    kin = k < p.K;
+    const int kc = min(k, p.K - 8);
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int c = tid + i * 256;
-      ra[i] = load_a<AMODE>(p, m0 + (c >> 3), kb + (c & 7) * 8);
+      ra[i] = ld8(a_ptr<AMODE>(p, min(m0 + (c >> 3), p.M - 1), kc));
     }
-    if constexpr (NORM) {
-      const int k = kb + (tid & 7) * 8;
-      rw = k < p.K ? ld8(p.norm_w + k) : bf16x8{};
-    }
+    if constexpr (NORM) rw = ld8(p.norm_w + kc);
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
       const int c = tid + i * 256;
-      const int n = n0 + (c >> 3), k = kb + (c & 7) * 8;
-      rb[i] = (n < p.N && k < p.K) ? ld8(p.b + (long)n * p.ldb + k) : bf16x8{};
+      rb[i] = ld8(p.b + (long)min(n0 + (c >> 3), p.N - 1) * p.ldb + kc);
     }
   };
-  auto sstore = [&](int buf) {
+  auto sstore = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < A_CH; ++i) {
       const int c = tid + i * 256;
-      bf16x8 v = ra[i];
+      bf16x8 v = kin ? ra[i] : bf16x8{};
       if constexpr (NORM) {
         // torch 2.10 nn.RMSNorm on bf16: fp32 x * rsqrt(.) * w, one rounding
         const float rs = s_rs[c >> 3];
@@ -370,7 +407,8 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
 #pragma unroll
     for (int i = 0; i < B_CH; ++i) {
       const int c = tid + i * 256;
-      *reinterpret_cast<bf16x8*>(&sB[buf][(c >> 3) * LDS_STRIDE + (c & 7) * 8]) = rb[i];
+      *reinterpret_cast<bf16x8*>(&sB[buf][(c >> 3) * LDS_STRIDE + (c & 7) * 8]) =
+          kin ? rb[i] : bf16x8{};
     }
   };
 
@@ -420,37 +458,39 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
   constexpr int RUN_STRIDE = MF == 32 ? 8 : 0;
   const int col_in = 4 * (lane / MF);
 
-  // ---- epilogue
+  // ---- epilogue, one column tile at a time: all loads, then all stores
+  constexpr bool PAIRED = EPI == EPI_ROPE || EPI == EPI_SILU;
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) {
-    const int m = m0 + wm * WM + tm * MF + (lane % MF);
-    if (m >= p.M) continue;
+  for (int tn = 0; tn < TN; ++tn) {
+    // paired epilogues: the first half of each 64-column block pairs with the
+    // tile 32 columns on
+    if (PAIRED && ((tn * MF) & 63) >= 32) continue;
+    constexpr int G = TM * RUNS;
+    int gm[G], gn[G];
+    EpiIn e[G];
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) {
+    for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
       for (int q = 0; q < RUNS; ++q) {
-        const int n = n0 + wn * WN + tn * MF + q * RUN_STRIDE + col_in;
-        if constexpr (EPI == EPI_ROPE || EPI == EPI_SILU) {
-          // first half of each 64-column block pairs with the tile 32 columns on
-          if (((tn * MF) & 63) >= 32 || n >= p.N) continue;
-          float x1[4], x2[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            x1[i] = acc[tn][tm][4 * q + i] * p.alpha;
-            x2[i] = acc[tn + PAIR_T][tm][4 * q + i] * p.alpha;
-          }
-          if constexpr (EPI == EPI_ROPE) epi_rope(p, m, n, x1, x2);
-          else epi_silu(p, m, n, x1, x2);
-        } else {
-          if (n >= p.N) continue;
-          float v[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][4 * q + i] * p.alpha;
-          if constexpr (EPI == EPI_EULER) epi_euler(p, m, n, v);
-          else epi_store<ACT>(p, m, n, v);
-        }
+        gm[tm * RUNS + q] = min(m0 + wm * WM + tm * MF + (lane % MF), p.M - 1);
+        gn[tm * RUNS + q] = min(n0 + wn * WN + tn * MF + q * RUN_STRIDE + col_in, p.N - 4);
       }
-    }
+    epi_load_groups<EPI, G>(p, gm, gn, e);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int q = 0; q < RUNS; ++q) {
+        const int m = m0 + wm * WM + tm * MF + (lane % MF);
+        const int n = n0 + wn * WN + tn * MF + q * RUN_STRIDE + col_in;
+        if (m >= p.M || n >= p.N) continue;
+        float x1[4], x2[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x1[i] = acc[tn][tm][4 * q + i] * p.alpha;
+          x2[i] = PAIRED ? acc[(tn + PAIR_T) % TN][tm][4 * q + i] * p.alpha : 0.f;
+        }
+        epi_apply<EPI, ACT>(p, m, n, x1, x2, e[tm * RUNS + q]);
+      }
   }
 }
 
@@ -539,7 +579,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
     b_slot[j] = pswz(r, lane & 3);
   }
 
-  auto issue = [&](auto SI, int kt) {
+  auto issue = [&](auto SI, int kt) __attribute__((always_inline)) {
     constexpr int S = decltype(SI)::value;
     bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
     bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
@@ -606,7 +646,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
         acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[tn], fx[tm], acc[tn][tm], 0, 0, 0);
   };
 
-  auto compute = [&](auto SI, int kt) {
+  auto compute = [&](auto SI, int kt) __attribute__((always_inline)) {
     constexpr int S = decltype(SI)::value;
     const bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
     const bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
@@ -676,34 +716,35 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
     mma(fw, fx);
   }
 
-  // ---- epilogue (same lane layout as gemm_kernel with MF = 16)
+  // ---- epilogue (same lane layout as gemm_kernel with MF = 16), one column
+  // tile at a time: all loads, then all stores
+  constexpr bool PAIRED = EPI == EPI_ROPE || EPI == EPI_SILU;
   const int col_in = 4 * g;
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) {
-    const int m = m0 + wm * WM + tm * 16 + fr;
-    if (m >= p.M) continue;
+  for (int tn = 0; tn < TN; ++tn) {
+    // paired epilogues: the first half of each 64-column block pairs with the
+    // tile 32 columns on
+    if (PAIRED && (tn & 3) >= 2) continue;
+    const int n = n0 + wn * WN + tn * 16 + col_in;
+    int gm[TM], gn[TM];
+    EpiIn e[TM];
 #pragma unroll
-    for (int tn = 0; tn < TN; ++tn) {
-      const int n = n0 + wn * WN + tn * 16 + col_in;
-      if constexpr (EPI == EPI_ROPE || EPI == EPI_SILU) {
-        // first half of each 64-column block pairs with the tile 32 columns on
-        if ((tn & 3) >= 2 || n >= p.N) continue;
-        float x1[4], x2[4];
+    for (int tm = 0; tm < TM; ++tm) {
+      gm[tm] = min(m0 + wm * WM + tm * 16 + fr, p.M - 1);
+      gn[tm] = min(n, p.N - 4);
+    }
+    epi_load_groups<EPI, TM>(p, gm, gn, e);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          x1[i] = acc[tn][tm][i] * p.alpha;
-          x2[i] = acc[tn + 2][tm][i] * p.alpha;
-        }
-        if constexpr (EPI == EPI_ROPE) epi_rope(p, m, n, x1, x2);
-        else epi_silu(p, m, n, x1, x2);
-      } else {
-        if (n >= p.N) continue;
-        float v[4];
+    for (int tm = 0; tm < TM; ++tm) {
+      const int m = m0 + wm * WM + tm * 16 + fr;
+      if (m >= p.M || n >= p.N) continue;
+      float x1[4], x2[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][i] * p.alpha;
-        if constexpr (EPI == EPI_EULER) epi_euler(p, m, n, v);
-        else epi_store<ACT>(p, m, n, v);
+      for (int i = 0; i < 4; ++i) {
+        x1[i] = acc[tn][tm][i] * p.alpha;
+        x2[i] = PAIRED ? acc[(tn + 2) % TN][tm][i] * p.alpha : 0.f;
       }
+      epi_apply<EPI, ACT>(p, m, n, x1, x2, e[tm]);
     }
   }
 }
@@ -741,6 +782,18 @@ __device__ __forceinline__ void mfma_agpr(f32x4& acc, const bf16x8& a, const bf1
   asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
 }
 
+// Redefines every accumulator (no instruction emitted): uses of acc after this
+// point depend on it, and volatile asm statements keep their relative order,
+// so reads cannot move above (and writes cannot move below) the neighbouring
+// s_nop wait states, which the compiler does not know the inline MFMAs need.
+template <int N1, int N2>
+__device__ __forceinline__ void pin_accumulators(f32x4 (&acc)[N1][N2]) {
+#pragma unroll
+  for (int i = 0; i < N1; ++i)
+#pragma unroll
+    for (int j = 0; j < N2; ++j) asm volatile("" : "+a"(acc[i][j]));
+}
+
 template <int AMODE, bool NORM, int EPI, int ACT>
 __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   static_assert(AMODE == A_DENSE && !NORM && EPI == EPI_STORE, "wide tile: plain dense GEMM");
@@ -772,7 +825,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   }
 
   // DMA j of a stage: j < W_DMA -> A block, else B block j - W_DMA
-  auto issue_one = [&](auto SI, int j, int kt) {
+  auto issue_one = [&](auto SI, int j, int kt) __attribute__((always_inline)) {
     constexpr int S = decltype(SI)::value;
     bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
     bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
@@ -784,7 +837,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
       __builtin_amdgcn_global_load_lds((void*)(b_src[j - W_DMA] + k),
                                        (lds_ptr_t)(sb + (wave * W_DMA + j - W_DMA) * 512), 16, 0, 0);
   };
-  auto issue = [&](auto SI, int kt) {
+  auto issue = [&](auto SI, int kt) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 2 * W_DMA; ++j) issue_one(SI, j, kt);
   };
@@ -799,7 +852,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   const int fr = lane & 15, g = lane >> 4;
   const int frag_off = fr * WBK + pswz(fr, g) * 8;  // pswz depends on fr only
   bf16x8 fw[2][WTN], fx[2][WTM];
-  auto read_one = [&](auto SI, auto RI, int f) {
+  auto read_one = [&](auto SI, auto RI, int f) __attribute__((always_inline)) {
     constexpr int S = decltype(SI)::value, R = decltype(RI)::value;
     const bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
     const bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
@@ -824,7 +877,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   // 64 MFMAs of stage s: refill stage s's buffer with K tile s + 4 (one DMA
   // every 4 MFMAs) and read stage s + 1's fragments into the other register
   // set (one every 2 MFMAs), so the reads have landed by the next step.
-  auto step = [&](auto SI, auto SN, auto RC, int kt) {
+  auto step = [&](auto SI, auto SN, auto RC, int kt) __attribute__((always_inline)) {
     constexpr int R = decltype(RC)::value;
     using RN = std::integral_constant<int, 1 - R>;
     __builtin_amdgcn_s_waitcnt(kWaitStep);
@@ -837,7 +890,10 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
     }
   };
 
-  // zeroed accumulators are written by VALU; the first MFMA reads them as srcC
+  // zeroed accumulators are written by VALU; the first MFMA reads them as
+  // srcC.  The empty asm statements redefine every accumulator, and volatile
+  // asm keeps its order, so the zeroing cannot sink below the wait states.
+  pin_accumulators(acc);
   asm volatile("s_nop 4");
   issue(I0{}, 0);
   issue(I1{}, 1);
@@ -857,21 +913,31 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   // let the last MFMAs retire before their accumulators are read
   __builtin_amdgcn_s_waitcnt(0);
   asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+  // no accumulator read may be scheduled above the wait states
+  pin_accumulators(acc);
 
   // ---- epilogue: lane holds C[m][n .. n+3], m = row fr of MFMA tile tm,
-  // n = 4 * g within MFMA tile tn
+  // n = 4 * g within MFMA tile tn; one column tile at a time: all loads, then
+  // all stores
 #pragma unroll
   for (int tn = 0; tn < WTN; ++tn) {
     const int n = n0 + wn * 128 + tn * 16 + 4 * g;
-    if (n >= p.N) continue;
+    int gm[WTM], gn[WTM];
+    EpiIn e[WTM];
+#pragma unroll
+    for (int tm = 0; tm < WTM; ++tm) {
+      gm[tm] = min(m0 + wm * 128 + tm * 16 + fr, p.M - 1);
+      gn[tm] = min(n, p.N - 4);
+    }
+    epi_load_groups<EPI, WTM>(p, gm, gn, e);
 #pragma unroll
     for (int tm = 0; tm < WTM; ++tm) {
       const int m = m0 + wm * 128 + tm * 16 + fr;
-      if (m >= p.M) continue;
+      if (m >= p.M || n >= p.N) continue;
       float v[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][i] * p.alpha;
-      epi_store<ACT>(p, m, n, v);
+      epi_apply<EPI, ACT>(p, m, n, v, v, e[tm]);
     }
   }
 }
@@ -885,14 +951,6 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
 // gathered while those loads are in flight.  The 8 partial tiles are summed
 // through LDS and all 512 threads run the epilogue.
 constexpr int SK_WAVES = 8;
-
-// 16-byte load that is always issued (address clamped into the tensor) and
-// zeroed when out of range: no divergent branch around the load.
-__device__ __forceinline__ bf16x8 ld8_or_zero(const bf16* base, long off, long off_clamped,
-                                              bool valid) {
-  const bf16x8 v = ld8(base + (valid ? off : off_clamped));
-  return valid ? v : bf16x8{};
-}
 
 template <int BN, int AMODE, bool NORM, int EPI, int ACT>
 __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
@@ -909,9 +967,12 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  const int nks = (p.K + 31) / 32;
-  const int per = (nks + SK_WAVES - 1) / SK_WAVES;
-  const int ks0 = wave * per, ks1 = min(nks, ks0 + per);
+  const int nkf = p.K / 32;  // full k-steps; a K % 32 tail is one extra step
+  // each wave takes whole rounds of KR k-steps (trailing waves may idle), so
+  // only the last round of the last busy wave reloads a step to fill up
+  const int rounds = (nkf + SK_WAVES * KR - 1) / (SK_WAVES * KR);
+  const int per = rounds * KR;
+  const int ks0 = wave * per, ks1 = min(nkf, ks0 + per);
   const int fr = lane & 15, fk = (lane >> 4) * 8;
 
   f32x4 acc[TN][TM];
@@ -920,94 +981,107 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Operand rows are clamped into the tensors (rows past M / N only feed
+  // outputs that are never stored) and k-steps past this wave's range reload
+  // its last step: every load of a round is issued unconditionally, so the
+  // whole round is in flight at once (a load under a branch would end its
+  // region with a full vmcnt(0) drain and serialise the round).
+  int a_rows[TM], b_rows[TN];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) a_rows[tm] = min(m0 + tm * 16 + fr, p.M - 1);
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) b_rows[tn] = min(n0 + tn * 16 + fr, p.N - 1);
+
   bf16x8 fw[KR][TN], fx[KR][TM], fg[KR];
-  auto load_round = [&](int base) {
+  auto load_step = [&](int r, int k) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
-      const int ks = base + r;
-      if (ks >= ks1) {  // wave-uniform: no loads for k-steps past this wave's range
+    for (int tn = 0; tn < TN; ++tn) fw[r][tn] = ld8(p.b + (long)b_rows[tn] * p.ldb + k);
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) fw[r][tn] = bf16x8{};
+    for (int tm = 0; tm < TM; ++tm) fx[r][tm] = ld8(a_ptr<AMODE>(p, a_rows[tm], k));
+    if constexpr (NORM) fg[r] = ld8(p.norm_w + k);
+  };
+  auto load_round = [&](int base) __attribute__((always_inline)) {
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm) fx[r][tm] = bf16x8{};
-        if constexpr (NORM) fg[r] = bf16x8{};
-        continue;
-      }
-      const int k = ks * 32 + fk;
-      const bool kin = k < p.K;
-      const int kc = min(k, p.K - 8);
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const int n = n0 + tn * 16 + fr;
-        const int nc = min(n, p.N - 1);
-        fw[r][tn] = ld8_or_zero(p.b, (long)n * p.ldb + k, (long)nc * p.ldb + kc, kin && n < p.N);
-      }
-#pragma unroll
-      for (int tm = 0; tm < TM; ++tm) {
-        if constexpr (AMODE == A_DENSE) {
-          const int m = m0 + tm * 16 + fr;
-          const int mc = min(m, p.M - 1);
-          fx[r][tm] = ld8_or_zero(p.a, (long)m * p.lda + k, (long)mc * p.lda + kc, kin && m < p.M);
-        } else {
-          fx[r][tm] = kin ? load_a<AMODE>(p, m0 + tm * 16 + fr, k) : bf16x8{};
-        }
-      }
-      if constexpr (NORM) fg[r] = ld8_or_zero(p.norm_w, k, kc, kin);
-    }
+    for (int r = 0; r < KR; ++r) load_step(r, min(base + r, ks1 - 1) * 32 + fk);
   };
   float rs[TM];
-  auto mma_round = [&](int base) {
+  auto mma_step = [&](int r) __attribute__((always_inline)) {
+    if constexpr (NORM) {
 #pragma unroll
-    for (int r = 0; r < KR; ++r) {
-      if (base + r >= ks1) break;  // wave-uniform
-      if constexpr (NORM) {
+      for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-          for (int j = 0; j < 8; ++j)
-            fx[r][tm][j] =
-                f2bf(__fmul_rn(__fmul_rn(bf2f(fx[r][tm][j]), rs[tm]), bf2f(fg[r][j])));
-      }
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-          acc[tn][tm] =
-              __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[r][tn], fx[r][tm], acc[tn][tm], 0, 0, 0);
+        for (int j = 0; j < 8; ++j)
+          fx[r][tm][j] = f2bf(__fmul_rn(__fmul_rn(bf2f(fx[r][tm][j]), rs[tm]), bf2f(fg[r][j])));
     }
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+        acc[tn][tm] =
+            __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[r][tn], fx[r][tm], acc[tn][tm], 0, 0, 0);
+  };
+  auto mma_round = [&](int base) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < KR; ++r)
+      if (base + r < ks1) mma_step(r);  // wave-uniform; only MFMAs under the branch
   };
 
-  load_round(ks0);
+  // row statistics (NORM): thread (row = tid / 8, part = tid % 8) sums chunks
+  // part, part + 8, ... of its row; its first 8 chunks are loaded before the
+  // first operand round so both are in flight together
+  constexpr int SB = 8;  // statistics chunks per thread per batch
+  const int srow = tid >> 3, spart = tid & 7;
+  const bf16* xr = p.a + (long)min(m0 + srow, p.M - 1) * p.lda;
+  bf16x8 sv[NORM ? SB : 1];
   if constexpr (NORM) {
-    // row statistics while the first round of operand loads is in flight:
-    // thread (row = tid / 8, part = tid % 8) sums chunks part, part + 8, ...
-    // of its row, accumulating as the loads land; 8 lanes then combine.
-    const int row = tid >> 3, part = tid & 7;
-    const int m = m0 + row;
-    const int mc = min(m, p.M - 1);
-    const bf16* xr = p.a + (long)mc * p.lda;
-    float ss = 0.f;
-#pragma unroll 4
-    for (int c = part * 8; c < p.K; c += 64) {
-      const bf16x8 v = ld8(xr + c);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float f = bf2f(v[e]);
-        ss += f * f;
+    for (int i = 0; i < SB; ++i) sv[i] = ld8(xr + min((spart + 8 * i) * 8, p.K - 8));
+  }
+  if (ks0 < ks1) load_round(ks0);
+  if constexpr (NORM) {
+    float ss = 0.f;
+    for (int c0 = 0;; c0 += SB * 64) {
+#pragma unroll
+      for (int i = 0; i < SB; ++i) {
+        const bool in = c0 + (spart + 8 * i) * 8 < p.K;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float f = in ? bf2f(sv[i][e]) : 0.f;
+          ss += f * f;
+        }
       }
+      if (c0 + SB * 64 >= p.K) break;
+#pragma unroll
+      for (int i = 0; i < SB; ++i)
+        sv[i] = ld8(xr + min(c0 + SB * 64 + (spart + 8 * i) * 8, p.K - 8));
     }
     ss += __shfl_xor(ss, 1, 64);
     ss += __shfl_xor(ss, 2, 64);
     ss += __shfl_xor(ss, 4, 64);
-    if (part == 0) s_rs[row] = 1.0f / sqrtf(ss / (float)p.K + p.norm_eps);
+    if (spart == 0) s_rs[srow] = 1.0f / sqrtf(ss / (float)p.K + p.norm_eps);
     __syncthreads();
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) rs[tm] = s_rs[tm * 16 + fr];
   }
-  mma_round(ks0);
-  for (int base = ks0 + KR; base < ks1; base += KR) {
-    load_round(base);
-    mma_round(base);
+  if (ks0 < ks1) {
+    mma_round(ks0);
+    for (int base = ks0 + KR; base < ks1; base += KR) {
+      load_round(base);
+      mma_round(base);
+    }
+  }
+  // K tail (K % 32 = 8, 16 or 24): the last wave adds one zero-filled step
+  if (nkf * 32 < p.K && wave == SK_WAVES - 1) {
+    const int k = nkf * 32 + fk;
+    const bool kin = k < p.K;
+    load_step(0, min(k, p.K - 8));
+    if (!kin) {
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) fw[0][tn] = bf16x8{};
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) fx[0][tm] = bf16x8{};
+    }
+    mma_step(0);
   }
 
   // partial tile: element (m_l, n_l) at s_part[wave][m_l * PS + n_l]
@@ -1019,7 +1093,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
           acc[tn][tm];
   __syncthreads();
 
-  auto sum4 = [&](int ml, int nl, float v[4]) {
+  auto sum4 = [&](int ml, int nl, float v[4]) __attribute__((always_inline)) {
     f32x4 t = *reinterpret_cast<const f32x4*>(&s_part[0][ml * PS + nl]);
 #pragma unroll
     for (int w = 1; w < SK_WAVES; ++w)
@@ -1027,30 +1101,32 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = t[i] * p.alpha;
   };
-  if constexpr (EPI == EPI_ROPE || EPI == EPI_SILU) {
-    constexpr int UPR = BN / 64 * 8;  // units per row: (64-block, 4-column group of the first half)
-    for (int u = tid; u < BM * UPR; u += NT) {
-      const int ml = u / UPR, r = u - ml * UPR;
-      const int nl = (r >> 3) * 64 + (r & 7) * 4;
-      const int m = m0 + ml, n = n0 + nl;
-      if (m >= p.M || n >= p.N) continue;
-      float x1[4], x2[4];
-      sum4(ml, nl, x1);
-      sum4(ml, nl + 32, x2);
-      if constexpr (EPI == EPI_ROPE) epi_rope(p, m, n, x1, x2);
-      else epi_silu(p, m, n, x1, x2);
-    }
-  } else {
-    constexpr int UPR = BN / 4;
-    for (int u = tid; u < BM * UPR; u += NT) {
-      const int ml = u / UPR, nl = (u - ml * UPR) * 4;
-      const int m = m0 + ml, n = n0 + nl;
-      if (m >= p.M || n >= p.N) continue;
-      float v[4];
-      sum4(ml, nl, v);
-      if constexpr (EPI == EPI_EULER) epi_euler(p, m, n, v);
-      else epi_store<ACT>(p, m, n, v);
-    }
+  // every thread handles ITER output groups: all their loads, then all stores
+  constexpr bool PAIRED = EPI == EPI_ROPE || EPI == EPI_SILU;
+  // units per row: 4-column groups (paired: of the first half of each 64-block)
+  constexpr int UPR = PAIRED ? BN / 64 * 8 : BN / 4;
+  constexpr int ITER = BM * UPR / NT;
+  static_assert(ITER * NT == BM * UPR, "epilogue units");
+  int ml[ITER], nl[ITER], gm[ITER], gn[ITER];
+  EpiIn e[ITER];
+#pragma unroll
+  for (int it = 0; it < ITER; ++it) {
+    const int u = tid + it * NT;
+    ml[it] = u / UPR;
+    const int r = u - ml[it] * UPR;
+    nl[it] = PAIRED ? (r >> 3) * 64 + (r & 7) * 4 : r * 4;
+    gm[it] = min(m0 + ml[it], p.M - 1);
+    gn[it] = min(n0 + nl[it], p.N - 4);
+  }
+  epi_load_groups<EPI, ITER>(p, gm, gn, e);
+#pragma unroll
+  for (int it = 0; it < ITER; ++it) {
+    const int m = m0 + ml[it], n = n0 + nl[it];
+    if (m >= p.M || n >= p.N) continue;
+    float x1[4], x2[4];
+    sum4(ml[it], nl[it], x1);
+    if constexpr (PAIRED) sum4(ml[it], nl[it] + 32, x2);
+    epi_apply<EPI, ACT>(p, m, n, x1, x2, e[it]);
   }
 }
 
@@ -1228,6 +1304,7 @@ int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void*
                      float norm_eps, svla_stream_t stream) {
   if (act < 0 || act > SVLA_ACT_SILU) return SVLA_EINVAL;
   if (out_f32 && (act || res)) return SVLA_EINVAL;
+  if (bias_f32 && !svla_aligned16(bias_f32)) return SVLA_EINVAL;
   GemmArgs p = base_args(a, lda, w, ldw, c, ldc, m, n, k);
   p.alpha = alpha;
   p.bias = static_cast<const bf16*>(bias);
@@ -1245,6 +1322,7 @@ int svla_linear_rope_bf16(const void* a, int lda, const void* w, int ldw, void* 
                           const float* sin_t, const void* norm_w, float norm_eps,
                           svla_stream_t stream) {
   if (!cos_t || !sin_t || rope_cols > n) return SVLA_EINVAL;
+  if (!svla_aligned16(cos_t) || !svla_aligned16(sin_t)) return SVLA_EINVAL;
   GemmArgs p = base_args(a, lda, w, ldw, c, ldc, m, n, k);
   p.rope_cos = cos_t;
   p.rope_sin = sin_t;
