@@ -232,6 +232,18 @@ int svla_time_embedding_bf16(double t, int dim, double min_period, double max_pe
 /* fp32 -> bf16 conversion (round to nearest even), n values. */
 int svla_f32_to_bf16(const float* x, void* y, long n, svla_stream_t stream);
 
+/* ------------------------------------------------------- pre-processing --
+ * Camera frames -> vision-encoder input: n uint8 RGB frames [h, w, 3]
+ * (HWC, frame stride src_bs bytes, host value h, w) resized with the aspect
+ * ratio kept to round((h, w) * min(S/h, S/w)) by bilinear interpolation
+ * (half-pixel centres, as torch interpolate(mode="bilinear",
+ * align_corners=False)), placed top-left in an S x S canvas padded with black,
+ * then mapped to [-1, 1] (x / 255 * 2 - 1) as bf16 [n, 3, S, S] (S = out_size).
+ * The "resize/normalize to [-1, 1]" step in front of the patch embedding; the
+ * reference feeds random images straight in (vla/vla.py:306, 396-408). */
+int svla_image_to_bf16(const uint8_t* src, long src_bs, int n, int h, int w, void* dst,
+                       int out_size, svla_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,7 @@ SIGNATURES = {
     "svla_embed_bf16": [_p, _p, _l, _i, _f, _p, _i, _l, _l, _i, _p],
     "svla_time_embedding_bf16": [_d, _i, _d, _d, _p, _p],
     "svla_f32_to_bf16": [_p, _p, _l, _p],
+    "svla_image_to_bf16": [_p, _l, _i, _i, _i, _p, _i, _p],
 }
 
 RESTYPES = {}

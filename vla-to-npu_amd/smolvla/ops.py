@@ -257,3 +257,18 @@ def f32_to_bf16(x, out=None):
     out = torch.empty(x.shape, dtype=BF16, device=x.device) if out is None else out
     _lib.call("svla_f32_to_bf16", _ptr(x), _ptr(out), x.numel(), _stream())
     return out
+
+
+def image_to_bf16(frames, out_size=512, out=None):
+    """uint8 RGB frames ``[n, h, w, 3]`` (GPU) -> bf16 ``[n, 3, S, S]`` in
+    [-1, 1], aspect-preserving bilinear resize with black padding
+    (``svla_image_to_bf16``)."""
+    if frames.dtype != torch.uint8 or frames.dim() != 4 or frames.shape[-1] != 3:
+        raise ValueError("frames must be uint8 [n, h, w, 3]")
+    frames = frames.contiguous()
+    n, h, w, _ = frames.shape
+    if out is None:
+        out = torch.empty(n, 3, out_size, out_size, dtype=BF16, device=frames.device)
+    _lib.call("svla_image_to_bf16", _ptr(frames), h * w * 3, n, h, w, _ptr(out), out_size,
+              _stream())
+    return out
