@@ -108,8 +108,8 @@ def dominant_kernel_roofline(eng, iters):
     tr = load_traffic()
     traffic = tr.get("bytes_per_launch") if tr and tr.get("shape") == [M, v.inter, v.hidden] else None
     return {
-        "kernel": "gemm_pipe_kernel<0, false, 0, 1> (A_DENSE, no norm, EPI_STORE, GELU_TANH: "
-                  "ViT MLP up-projection)",
+        "kernel": "gemm_pipe_kernel<128, 128, 0, false, 0, 1> (128x128 LDS-DMA pipeline, dense A, "
+                  "no norm, bias + tanh-GELU store: ViT MLP up-projection)",
         "shape": [M, v.inter, v.hidden],
         "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
@@ -155,6 +155,51 @@ def load_traffic():
         return None
 
 
+def traffic_summary(fetch_csv, write_csv, shape):
+    """Write the committed traffic record from the two ``--traffic-probe``
+    counter runs' ``*_counter_collection.csv`` files: per dispatch of the GEMM
+    and of the 1 GiB copy, FETCH_SIZE / WRITE_SIZE in KiB; each counter is
+    scaled so that the copy reads (resp. writes) exactly 1 GiB."""
+    import csv
+
+    def per_dispatch(path, counter):
+        vals = {}
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                if r.get("Counter_Name") != counter:
+                    continue
+                name = r["Kernel_Name"]
+                kind = "gemm" if "gemm" in name else "copy" if "copyBuffer" in name else None
+                if kind:
+                    key = (kind, r.get("Dispatch_Id") or r.get("Correlation_Id"))
+                    vals[key] = (name, vals.get(key, (name, 0.0))[1] + float(r["Counter_Value"]))
+        out = {"gemm": [], "copy": [], "name": None}
+        for (kind, _), (name, v) in sorted(vals.items(), key=lambda kv: int(kv[0][1])):
+            out[kind].append(v)
+            if kind == "gemm":
+                out["name"] = name
+        return out
+
+    fe, wr = per_dispatch(fetch_csv, "FETCH_SIZE"), per_dispatch(write_csv, "WRITE_SIZE")
+    gib_kib = float(1 << 20)
+    fscale = gib_kib / statistics.mean(fe["copy"])
+    wscale = gib_kib / statistics.mean(wr["copy"])
+    fb = statistics.mean(fe["gemm"]) * fscale * 1024
+    wb = statistics.mean(wr["gemm"]) * wscale * 1024
+    M, N, K = shape
+    kname = fe["name"].replace("(anonymous namespace)::", "").replace("void ", "")
+    rec = {"kernel": kname.split("(")[0].strip(), "shape": list(shape),
+           "fetch_kib_raw": [round(v, 1) for v in fe["gemm"]],
+           "write_kib_raw": [round(v, 1) for v in wr["gemm"]],
+           "copy_fetch_kib_raw": [round(v, 1) for v in fe["copy"]],
+           "copy_write_kib_raw": [round(v, 1) for v in wr["copy"]],
+           "fetch_scale": round(fscale, 4), "write_scale": round(wscale, 4),
+           "fetch_bytes": int(fb), "write_bytes": int(wb), "bytes_per_launch": int(fb + wb),
+           "algorithmic_bytes": 2.0 * (M * K + N * K + M * N + N)}
+    TRAFFIC_FILE.write_text(json.dumps(rec, indent=1) + "\n")
+    print(json.dumps(rec))
+
+
 def cpu_baseline(cfg, params, seconds):
     """CPU oracle (PyTorch bf16 restatement of the reference modules) on this
     host: bs=1 chunks until `seconds` of work (after one warm-up chunk)."""
@@ -191,6 +236,8 @@ def main():
     ap.add_argument("--no-latency", action="store_true")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="turn the two --traffic-probe counter CSVs into the committed record")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs on a single GPU "
@@ -205,6 +252,11 @@ def main():
     cfg = SmolVLAConfig()
     if args.traffic_probe:
         traffic_probe(cfg, args.batch)
+        return
+    if args.traffic_summary:
+        v = cfg.vit
+        traffic_summary(*args.traffic_summary,
+                        (args.batch * cfg.n_cameras * v.tokens, v.inter, v.hidden))
         return
     log("generating seeded random-init bf16 weights")
     params = smolvla_params(cfg, seed=0)

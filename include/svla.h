@@ -81,9 +81,13 @@ int svla_layernorm_bf16(const void* x, int ldx, const void* gamma, const void* b
  *   v = alpha*acc (+ bias[n]) (+ bias_f32[n]); if out_f32: store fp32 v.
  *   else v = bf16(v); v = bf16(act(v)); if res: v = bf16(v + res[m,n]); store.
  * bias/bias_f32/res may be NULL; res may alias c (in-place residual update).
- * K % 8 == 0, N % 4 == 0, aligned.  No workspace: problems with few rows
- * (M <= 256) split K across the waves of each workgroup instead of across
- * workgroups. */
+ * K % 8 == 0, N % 4 == 0, aligned.  Problems with few rows (M <= 256) split K
+ * across the 8 waves of each workgroup and, when that grid is far smaller than
+ * the chip, across workgroups too: the partial tiles go to a per-device
+ * workspace (allocated by the library on the first such call that is not being
+ * graph-captured, kept until exit) and the last workgroup of each tile sums
+ * them in a fixed order.  Such calls on different streams of one device must
+ * not overlap in time (svla_gemm_set_split(1) turns the split off). */
 int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
                      const float* bias_f32, const void* res, int ldr, void* c, int ldc, int m,
                      int n, int k, float alpha, int act, int out_f32, const void* norm_w,
@@ -96,6 +100,11 @@ int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void*
  * 4-stage LDS-DMA pipeline), or -1 for the automatic
  * shape-based choice (default).  Process-wide; not thread-safe. */
 int svla_gemm_set_tile(int tile);
+
+/* Tuning hook: force the number of cross-workgroup K splits of skinny
+ * (M <= 256) GEMMs, 1..64 (1 = never split), or -1 for the automatic choice
+ * (default).  Process-wide; not thread-safe. */
+int svla_gemm_set_split(int splits);
 
 /* Fused (RMSNorm +) QKV projection with rotate-half RoPE in the epilogue.
  * Columns [0, rope_cols) are heads of 64 that get RoPE at position

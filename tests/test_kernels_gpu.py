@@ -212,12 +212,64 @@ def force_tile(ops):
     lib.svla_gemm_set_tile(-1)
 
 
+@pytest.fixture
+def force_split(ops):
+    from smolvla import _lib
+    lib = _lib.load()
+    yield lambda s: lib.svla_gemm_set_split(s)
+    lib.svla_gemm_set_split(-1)
+
+
 @pytest.mark.parametrize("tile", sorted(TILES))
 def test_every_tile_config_every_epilogue(ops, force_tile, tile):
     """Each GEMM kernel configuration, forced, on ragged shapes (M, N, K
     tails) through every epilogue, the fused RMSNorm and both A gathers."""
-    g = gen(100 + tile)
     force_tile(tile)
+    _every_epilogue(ops, gen(100 + tile), tile)
+
+
+@pytest.mark.parametrize("tile,splits", [(4, 2), (5, 3), (4, 6), (5, 8)])
+def test_skinny_split_k_every_epilogue(ops, force_tile, force_split, tile, splits):
+    """Skinny kernels with K split over `splits` workgroups (partials summed
+    by the last one to arrive), through every epilogue and gather; the K tail
+    lands in the last split."""
+    force_tile(tile)
+    force_split(splits)
+    _every_epilogue(ops, gen(200 + 10 * tile + splits), tile)
+
+
+def test_skinny_split_k_graph_replays(ops, force_split):
+    """Split-K calls captured in a graph: several replays with eager work in
+    between, every replay equal to the eager result (the arrival counters are
+    reset by each call), then a smaller problem on the same workspace."""
+    g = gen(31)
+    force_split(4)
+    a, w = randn(g, 50, 2048), randn(g, 2048, 720, std=0.02)
+    res = randn(g, 50, 720)
+    a, wp, res = a.cuda(), ops.pack_weight(w.cuda()), res.cuda()
+    want = ref.linear(a.cpu(), w) + res.cpu()
+    out = torch.empty(50, 720, dtype=BF16, device="cuda")
+    eager = ops.linear(a, wp, res=res)
+    assert_close_bf16(eager, want)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.linear(a, wp, res=res, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.linear(a, wp, res=res, out=out)
+    for rep in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {rep}"
+        ops.linear(a[:17], wp, out=torch.empty(17, 720, dtype=BF16, device="cuda"))
+    small = ops.linear(a[:9, :1536], ops.pack_weight(w[:1536].cuda()))
+    assert_close_bf16(small, ref.linear(a[:9, :1536].cpu(), w[:1536]))
+
+
+def _every_epilogue(ops, g, tile):
     M, K = 200, 200                                   # K tail (200 = 6*32 + 8)
     x = randn(g, M, K)
     nw = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16)

@@ -37,6 +37,8 @@
 //  * Workgroup ids are remapped so consecutive tiles land on the same XCD
 //    (the hardware deals workgroups round-robin over the 8 XCDs, each with its
 //    own L2): neighbouring tiles share A rows in that XCD's L2.
+#include <mutex>
+
 #include "svla_common.h"
 
 namespace {
@@ -81,6 +83,10 @@ struct GemmArgs {
   // fused RMSNorm of the A rows: a = bf16(x * rsqrt(mean(x^2) + eps) * w[k])
   const bf16* norm_w;
   float norm_eps;
+  // skinny split-K (gridDim.z > 1): fp32 partial tiles [tile][split][BM * BN]
+  // and one arrival counter per output tile (zero between calls)
+  float* ws;
+  unsigned* ws_cnt;
 };
 
 __device__ __forceinline__ long crow(const GemmArgs& p, int m) {
@@ -950,6 +956,13 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
 // at once before any MFMA, and the optional RMS statistics of the A rows are
 // gathered while those loads are in flight.  The 8 partial tiles are summed
 // through LDS and all 512 threads run the epilogue.
+//
+// Split-K over workgroups (gridDim.z = S > 1, for long-K problems whose grid
+// is far smaller than the chip): workgroup z covers k-steps
+// [z * kps, (z + 1) * kps) and writes its fp32 tile to the workspace; the
+// last of the S workgroups of a tile to arrive (device-scope counter) sums the
+// S partials in split order, runs the epilogue and resets the counter.  No
+// workgroup ever waits for another.
 constexpr int SK_WAVES = 8;
 
 template <int BN, int AMODE, bool NORM, int EPI, int ACT>
@@ -964,15 +977,19 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
   static_assert(!NORM || AMODE == A_DENSE, "row norm only for dense A");
   __shared__ __attribute__((aligned(16))) float s_part[SK_WAVES][BM * PS];
   __shared__ float s_rs[NORM ? BM : 1];
+  __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int nkf = p.K / 32;  // full k-steps; a K % 32 tail is one extra step
+  const int S = gridDim.z, z = blockIdx.z;
+  const int kps = (nkf + S - 1) / S;  // k-steps of one split
+  const int kb = min(nkf, z * kps), ke = min(nkf, kb + kps);
   // each wave takes whole rounds of KR k-steps (trailing waves may idle), so
   // only the last round of the last busy wave reloads a step to fill up
-  const int rounds = (nkf + SK_WAVES * KR - 1) / (SK_WAVES * KR);
+  const int rounds = (ke - kb + SK_WAVES * KR - 1) / (SK_WAVES * KR);
   const int per = rounds * KR;
-  const int ks0 = wave * per, ks1 = min(nkf, ks0 + per);
+  const int ks0 = kb + wave * per, ks1 = min(ke, ks0 + per);
   const int fr = lane & 15, fk = (lane >> 4) * 8;
 
   f32x4 acc[TN][TM];
@@ -1070,8 +1087,9 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
       mma_round(base);
     }
   }
-  // K tail (K % 32 = 8, 16 or 24): the last wave adds one zero-filled step
-  if (nkf * 32 < p.K && wave == SK_WAVES - 1) {
+  // K tail (K % 32 = 8, 16 or 24): the last wave of the last split adds one
+  // zero-filled step
+  if (nkf * 32 < p.K && wave == SK_WAVES - 1 && z == S - 1) {
     const int k = nkf * 32 + fk;
     const bool kin = k < p.K;
     load_step(0, min(k, p.K - 8));
@@ -1093,11 +1111,62 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
           acc[tn][tm];
   __syncthreads();
 
-  auto sum4 = [&](int ml, int nl, float v[4]) __attribute__((always_inline)) {
+  auto wave_sum4 = [&](int ml, int nl) __attribute__((always_inline)) {
     f32x4 t = *reinterpret_cast<const f32x4*>(&s_part[0][ml * PS + nl]);
 #pragma unroll
     for (int w = 1; w < SK_WAVES; ++w)
       t += *reinterpret_cast<const f32x4*>(&s_part[w][ml * PS + nl]);
+    return t;
+  };
+  constexpr int G4 = BM * BN / 4;  // 4-column groups of the tile
+  if (S > 1) {
+    const int tile = blockIdx.y * gridDim.x + blockIdx.x;
+    float* wt = p.ws + (long)tile * S * (BM * BN);
+    // The partials are written and read with device-scope accesses, which
+    // go through to the memory side instead of staying in one XCD's L2, and
+    // every store is acknowledged (vmcnt = 0) before the barrier that
+    // precedes this tile's counter increment: a workgroup that sees the
+    // count reach S - 1 therefore reads every split's finished partial.
+    // (A device-scope release/acquire fence pair orders the same way but
+    // writes back and invalidates the whole L2 of each XCD: up to 5 us per
+    // call at these sizes, measured on MI355X.)
+    for (int u = tid; u < G4; u += NT) {
+      const int ml = u / (BN / 4), nl = (u - ml * (BN / 4)) * 4;
+      const f32x4 v = wave_sum4(ml, nl);
+      float* d = wt + (long)z * (BM * BN) + ml * BN + nl;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        __hip_atomic_store(d + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __syncthreads();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(p.ws_cnt + tile, 1u, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(S - 1);
+    __syncthreads();
+    if (!s_last) return;
+    // the total goes to wave 0's slot; the epilogue below then reads slot 0
+    // only (sum in split order: the result does not depend on arrival order)
+    for (int u = tid; u < G4; u += NT) {
+      const int ml = u / (BN / 4), nl = (u - ml * (BN / 4)) * 4;
+      f32x4 t = {0.f, 0.f, 0.f, 0.f};
+      for (int zz = 0; zz < S; ++zz) {
+        const float* q = wt + (long)zz * (BM * BN) + ml * BN + nl;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          t[i] += __hip_atomic_load(q + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      *reinterpret_cast<f32x4*>(&s_part[0][ml * PS + nl]) = t;
+    }
+    if (tid == 0)  // ready for the next call
+      __hip_atomic_store(p.ws_cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+  }
+  auto sum4 = [&](int ml, int nl, float v[4]) __attribute__((always_inline)) {
+    const f32x4 t = S > 1 ? *reinterpret_cast<const f32x4*>(&s_part[0][ml * PS + nl])
+                          : wave_sum4(ml, nl);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = t[i] * p.alpha;
   };
@@ -1228,6 +1297,68 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain) {
   return pipe_ok ? tile_dims(P64) : tile_dims(T64);
 }
 
+// ---- skinny split-K --------------------------------------------------------
+// Workspace: one per device, allocated on the first split call that is not
+// being captured into a graph and kept for the life of the process (a split
+// call on a capturing stream before that runs unsplit).  All split calls on a
+// device share it, so such calls on different streams must not overlap in
+// time; calls on one stream, and replays of graphs captured from them, are
+// ordered.  svla_gemm_set_split(1) turns splitting off.
+constexpr size_t kWsFloats = (size_t)4 << 20;  // 16 MB of fp32 partial tiles
+constexpr int kWsTiles = 4096;                 // arrival counters
+constexpr int kMaxDevices = 64;
+struct SplitWs {
+  float* part;
+  unsigned* cnt;
+};
+SplitWs g_ws[kMaxDevices];
+std::mutex g_ws_mu;
+int g_force_split = -1;  // svla_gemm_set_split: -1 = automatic
+
+const SplitWs* split_ws(hipStream_t s) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  SplitWs& w = g_ws[dev];
+  if (w.part) return &w;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+  float* part = nullptr;
+  unsigned* cnt = nullptr;
+  if (hipMalloc(&part, kWsFloats * sizeof(float)) != hipSuccess) return nullptr;
+  if (hipMalloc(&cnt, kWsTiles * sizeof(unsigned)) != hipSuccess ||
+      hipMemset(cnt, 0, kWsTiles * sizeof(unsigned)) != hipSuccess) {
+    (void)hipFree(part);
+    if (cnt) (void)hipFree(cnt);
+    return nullptr;
+  }
+  w.part = part;
+  w.cnt = cnt;
+  return &w;
+}
+
+// Number of K splits for a skinny grid of `tiles` workgroups.  Measured on
+// MI355X (bs=1 expert, prefix and connector shapes): a split costs ~1-2 us of
+// partial stores, counter round trip and partial loads, which only long K
+// repays -- K = 2048 at 23 tiles: 12.7 -> 10.2 us (S = 4); K = 2560 at 120
+// tiles: 17.5 -> 14.3 us (S = 2); K = 12288 at 90 tiles: 69 -> 40 us (S = 2);
+// K <= 960 always lost.  So: K >= 1536, at most one workgroup per CU, and at
+// least 16 k-steps of 32 per split.
+int pick_split(int tiles, int K, int bm, int bn) {
+  const int nkf = K / 32;
+  int S;
+  if (g_force_split >= 1) {
+    S = g_force_split;
+  } else {
+    if (K < 1536) return 1;
+    S = min(kNumCU / tiles, nkf / 16);
+  }
+  S = min(S, max(1, nkf));
+  // workspace capacity
+  while (S > 1 && ((size_t)tiles * S * bm * bn > kWsFloats || tiles > kWsTiles)) --S;
+  return max(S, 1);
+}
+
 template <int AMODE, bool NORM>
 int dispatch(const GemmArgs& p, int epi, int act, TileId t, dim3 grid, hipStream_t s) {
   switch (epi) {
@@ -1264,6 +1395,15 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
   if (p.norm_w && p.K > 2048) return SVLA_EINVAL;  // row statistics keep <= 2048 per row
   const int gm = (p.M + t.bm - 1) / t.bm, gn = (p.N + t.bn - 1) / t.bn;
   dim3 grid(gn, gm, 1);
+  if (t.id == S32 || t.id == S64) {
+    const int S = pick_split(gm * gn, p.K, t.bm, t.bn);
+    const SplitWs* w = S > 1 ? split_ws(s) : nullptr;
+    if (w) {
+      p.ws = w->part;
+      p.ws_cnt = w->cnt;
+      grid.z = S;
+    }
+  }
   if constexpr (AMODE == A_DENSE) {
     if (p.norm_w) return dispatch<AMODE, true>(p, epi, act, t.id, grid, s);
   }
@@ -1295,6 +1435,12 @@ int svla_version(void) { return 200; }
 int svla_gemm_set_tile(int tile) {
   if (tile < -1 || tile >= NUM_TILES) return SVLA_EINVAL;
   g_force_tile = tile;
+  return SVLA_OK;
+}
+
+int svla_gemm_set_split(int splits) {
+  if (splits < -1 || splits == 0 || splits > 64) return SVLA_EINVAL;
+  g_force_split = splits;
   return SVLA_OK;
 }
 
