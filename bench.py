@@ -107,9 +107,14 @@ def dominant_kernel_roofline(eng, iters):
     hbm_bytes = 2.0 * (M * v.hidden + v.inter * v.hidden + M * v.inter + v.inter)
     tr = load_traffic()
     traffic = tr.get("bytes_per_launch") if tr and tr.get("shape") == [M, v.inter, v.hidden] else None
+    from smolvla import _lib
+    tile = _lib.load().svla_gemm_tile_choice(M, v.inter, v.hidden, 1)
+    kname = {8: "gemm_wide_kernel<0, false, 0, 1> (256x256 tile, 4-stage LDS-DMA ring, "
+                "LDS-staged bias + tanh-GELU epilogue)",
+             7: "gemm_pipe_kernel<128, 128, 0, false, 0, 1> (128x128 LDS-DMA pipeline, "
+                "bias + tanh-GELU epilogue)"}.get(tile, f"GEMM tile configuration {tile}")
     return {
-        "kernel": "gemm_pipe_kernel<128, 128, 0, false, 0, 1> (128x128 LDS-DMA pipeline, dense A, "
-                  "no norm, bias + tanh-GELU store: ViT MLP up-projection)",
+        "kernel": kname + ": ViT MLP up-projection",
         "shape": [M, v.inter, v.hidden],
         "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),

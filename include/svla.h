@@ -101,6 +101,11 @@ int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void*
  * shape-based choice (default).  Process-wide; not thread-safe. */
 int svla_gemm_set_tile(int tile);
 
+/* Query: the tile configuration (numbering of svla_gemm_set_tile) that
+ * svla_linear_bf16 picks for a dense, un-normalised, packed (ldc = n) problem
+ * of this shape, or SVLA_EINVAL.  For reports and tests. */
+int svla_gemm_tile_choice(int m, int n, int k, int act);
+
 /* Tuning hook: force the number of cross-workgroup K splits of skinny
  * (M <= 256) GEMMs, 1..64 (1 = never split), or -1 for the automatic choice
  * (default).  Process-wide; not thread-safe. */

@@ -129,12 +129,13 @@ def test_linear_bias_act_residual(ops):
     assert rel_err(got, want) < 1e-3
 
 
-@pytest.mark.parametrize("M,N,K", [(300, 260, 128), (1000, 700, 384), (513, 1028, 768),
-                                   (256, 256, 3072)])
+@pytest.mark.parametrize("M,N,K", [(300, 264, 128), (1000, 704, 384), (513, 1032, 768),
+                                   (256, 256, 3072), (300, 260, 128)])
 def test_wide_tile_forced(ops, force_tile, M, N, K):
-    """The 256x256 wide kernel (K % 128 == 0) on ragged M / N tails, through
-    the plain epilogues it serves: bias + GELU, bias + residual, alpha, fp32
-    out with fp32 bias."""
+    """The 256x256 wide kernel (K % 128 == 0, N % 8 == 0) on ragged M / N
+    tails, through the plain epilogues it serves: bias + GELU, bias +
+    residual (also in place), alpha, fp32 bias, fp32 out (which, like
+    N % 8 != 0, takes the 128x128 pipeline instead)."""
     g = gen(M + N + K)
     force_tile(8)
     a, w, b = randn(g, M, K), randn(g, K, N, std=0.05), randn(g, N, std=0.05)
@@ -145,7 +146,12 @@ def test_wide_tile_forced(ops, force_tile, M, N, K):
     assert_close_bf16(ops.linear(a.cuda(), wp, bias=b.cuda(), res=res.cuda()),
                       ref.linear(a, w, b) + res)
     assert_close_bf16(ops.linear(a.cuda(), wp, alpha=0.125), (ref.linear(a, w).float() * 0.125))
+    inplace = res.cuda()
+    ops.linear(a.cuda(), wp, res=inplace, out=inplace)
+    assert_close_bf16(inplace, ref.linear(a, w) + res)
     bf = torch.randn(N, generator=g) * 0.1
+    assert_close_bf16(ops.linear(a.cuda(), wp, bias_f32=bf.cuda()),
+                      (a.float() @ w.float() + bf).to(BF16))
     got = ops.linear(a.cuda(), wp, bias_f32=bf.cuda(), out_f32=True)
     assert rel_err(got, a.float() @ w.float() + bf) < 1e-3
 

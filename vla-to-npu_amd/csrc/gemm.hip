@@ -922,28 +922,104 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   // no accumulator read may be scheduled above the wait states
   pin_accumulators(acc);
 
-  // ---- epilogue: lane holds C[m][n .. n+3], m = row fr of MFMA tile tm,
-  // n = 4 * g within MFMA tile tn; one column tile at a time: all loads, then
-  // all stores
+  // ---- epilogue, staged through LDS so that every global store writes whole
+  // 128-byte lines.  In the MFMA layout a lane holds C[m][n .. n+3] for 16
+  // different rows per instruction, i.e. 32-byte pieces of 16 lines, which the
+  // memory side writes back as partial lines (measured: ~5x slower than
+  // line-sized stores and 1.3x the bytes).
+  // Phase 1 (MFMA layout): v = bf16(act(bf16(alpha * acc + bias))) goes to the
+  // wave's private 128 x 128 bf16 tile in LDS (the ring is free once every
+  // wave is past its last fragment read: the barrier below).  Row r of the
+  // tile is 32 chunks of 4 columns; chunk c sits in slot c ^ ((r & 7) << 2),
+  // so the 16 rows x 4 chunks of one write fall on distinct banks pairwise.
+  // Phase 2 (row layout): 16 lanes read a 256-byte row (one 16-byte read
+  // each, contiguous slots since the swizzle keeps bit 0), add the row-wise
+  // operands (position addend, residual) and store it with 16-byte stores.
+  __builtin_amdgcn_s_barrier();
+  bf16* st_lo = wave == 0 ? sA0 : wave == 1 ? sA2 : wave == 2 ? sB0 : sB2;  // rows 0 .. 63
+  bf16* st_hi = wave == 0 ? sA1 : wave == 1 ? sA3 : wave == 2 ? sB1 : sB3;  // rows 64 .. 127
+  auto st_addr = [&](int r, int chunk) __attribute__((always_inline)) {
+    return (r < 64 ? st_lo : st_hi) + (r & 63) * 128 + ((chunk ^ ((r & 7) << 2)) << 2);
+  };
+  const int wm0 = m0 + wm * 128, wn0 = n0 + wn * 128;
+  // per-column addend: bf16 bias + fp32 bias, summed once (fp32)
+  f32x4 cb[WTN];
+#pragma unroll
+  for (int tn = 0; tn < WTN; ++tn) cb[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (p.bias) {
+#pragma unroll
+    for (int tn = 0; tn < WTN; ++tn) {
+      const bf16x4 b4 = *reinterpret_cast<const bf16x4*>(p.bias + min(wn0 + tn * 16 + 4 * g, p.N - 4));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cb[tn][i] = bf2f(b4[i]);
+    }
+  }
+  if (p.bias_f32) {
+#pragma unroll
+    for (int tn = 0; tn < WTN; ++tn)
+      cb[tn] += *reinterpret_cast<const f32x4*>(p.bias_f32 + min(wn0 + tn * 16 + 4 * g, p.N - 4));
+  }
+  const float alpha = p.alpha;
 #pragma unroll
   for (int tn = 0; tn < WTN; ++tn) {
-    const int n = n0 + wn * 128 + tn * 16 + 4 * g;
-    int gm[WTM], gn[WTM];
-    EpiIn e[WTM];
 #pragma unroll
     for (int tm = 0; tm < WTM; ++tm) {
-      gm[tm] = min(m0 + wm * 128 + tm * 16 + fr, p.M - 1);
-      gn[tm] = min(n, p.N - 4);
+      bf16x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = __builtin_fmaf(acc[tn][tm][i], alpha, cb[tn][i]);
+        if constexpr (ACT != SVLA_ACT_NONE) o[i] = f2bf(apply_act<ACT>(rbf(v)));
+        else o[i] = f2bf(v);
+      }
+      *reinterpret_cast<bf16x4*>(st_addr(tm * 16 + fr, tn * 4 + g)) = o;
     }
-    epi_load_groups<EPI, WTM>(p, gm, gn, e);
+    // keep the next column tile's accumulator reads below this tile's LDS
+    // writes (otherwise the scheduler hoists all 256 AGPR reads up front and
+    // runs out of VGPRs)
+    if (tn + 1 < WTN) {
+      asm volatile("" ::: "memory");
 #pragma unroll
-    for (int tm = 0; tm < WTM; ++tm) {
-      const int m = m0 + wm * 128 + tm * 16 + fr;
-      if (m >= p.M || n >= p.N) continue;
-      float v[4];
+      for (int tm = 0; tm < WTM; ++tm) asm volatile("" : "+a"(acc[tn + 1][tm]));
+    }
+  }
+  // the same wave reads back what its lanes wrote (LDS operations of a wave
+  // complete in order)
+  constexpr int kRowsPerPass = 4, kPasses = 128 / kRowsPerPass, kBatch = 8;
+  const int j = lane & 15;
+  const int n = wn0 + 8 * j;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = acc[tn][tm][i] * p.alpha;
-      epi_apply<EPI, ACT>(p, m, n, v, v, e[tm]);
+  for (int b0 = 0; b0 < kPasses; b0 += kBatch) {
+    bf16x8 v[kBatch], ad[kBatch], rs[kBatch];
+    int m[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      const int r = (b0 + b) * kRowsPerPass + (lane >> 4);
+      m[b] = wm0 + r;
+      v[b] = *reinterpret_cast<const bf16x8*>(st_addr(r, 2 * j));
+    }
+    if (p.rowadd) {
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b)
+        ad[b] = ld8(p.rowadd + (long)(min(m[b], p.M - 1) % p.rowadd_period) * p.N + min(n, p.N - 8));
+    }
+    if (p.res) {
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b)
+        rs[b] = ld8(p.res + (long)min(m[b], p.M - 1) * p.ldr + min(n, p.N - 8));
+    }
+#pragma unroll
+    for (int b = 0; b < kBatch; ++b) {
+      if (m[b] >= p.M || n >= p.N) continue;
+      bf16x8 o = v[b];
+      if (p.rowadd) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(ad[b][i]));
+      }
+      if (p.res) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rs[b][i]));
+      }
+      st8(reinterpret_cast<bf16*>(p.c) + crow(p, m[b]) * p.ldc + n, o);
     }
   }
 }
@@ -1267,11 +1343,12 @@ TileCfg tile_dims(TileId id) {
 }
 
 // `plain`: dense A, no fused norm, plain store epilogue (the wide kernel's scope)
-TileCfg pick_tile(int M, int N, int K, int epi, bool plain) {
+TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok) {
   auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   const bool paired = epi == EPI_ROPE || epi == EPI_SILU;
   const bool pipe_ok = K >= PBK;  // the pipelined kernels need one full K step
-  const bool wide_ok = plain && K % (4 * WBK) == 0;  // whole 4-stage rounds
+  // whole 4-stage rounds; 16-byte row stores (N, ldc, ldr multiples of 8)
+  const bool wide_ok = plain && K % (4 * WBK) == 0 && wide_rows_ok;
   if (g_force_tile >= 0 && !(paired && g_force_tile == S32)) {
     if (g_force_tile == W256 && !wide_ok) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
     if (g_force_tile == P128 && !pipe_ok) return tile_dims(T128);
@@ -1284,10 +1361,10 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain) {
   }
   // measured on MI355X: 128x128 tiles win once the grid has ~4 waves of
   // workgroups; below that the 64x64 tile's larger grid wins
-  // measured on MI355X (M = 98304): the wide tile wins at K = 3072 (+21%) and
-  // ties or loses at K = 768, where its per-tile pipeline fill and epilogue
-  // weigh more
-  if (wide_ok && K >= 1536 && tiles(WBM, WBN) >= 2 * kNumCU) return tile_dims(W256);
+  // measured on MI355X (M = 98304, N = 3072): with its LDS-staged epilogue the
+  // wide tile beats the 128x128 pipeline from K = 512 (K = 768 + GELU: 675 vs
+  // 752 us; K = 3072: 1603 vs 2285 us) and loses below (K = 256: 465 vs 430)
+  if (wide_ok && K >= 512 && tiles(WBM, WBN) >= 2 * kNumCU) return tile_dims(W256);
   if (M >= 4096 || tiles(128, 128) >= 4 * kNumCU) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
   // mid-size (the batched expert, M = 1600), measured on MI355X: with at least
   // one 128x128 tile per CU the 32x32-MFMA register-staged 128x128 kernel wins
@@ -1391,7 +1468,10 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
   if (p.norm_w && (AMODE != A_DENSE || !svla_aligned16(p.norm_w))) return SVLA_EINVAL;
 
   const bool plain = AMODE == A_DENSE && !p.norm_w && epi == EPI_STORE;
-  const TileCfg t = pick_tile(p.M, p.N, p.K, epi, plain);
+  const bool wide_rows_ok = !p.out_f32 && p.N % 8 == 0 && p.ldc % 8 == 0 &&
+                            (!p.res || (p.ldr % 8 == 0 && svla_aligned16(p.res))) &&
+                            (!p.rowadd || svla_aligned16(p.rowadd));
+  const TileCfg t = pick_tile(p.M, p.N, p.K, epi, plain, wide_rows_ok);
   if (p.norm_w && p.K > 2048) return SVLA_EINVAL;  // row statistics keep <= 2048 per row
   const int gm = (p.M + t.bm - 1) / t.bm, gn = (p.N + t.bn - 1) / t.bn;
   dim3 grid(gn, gm, 1);
@@ -1436,6 +1516,12 @@ int svla_gemm_set_tile(int tile) {
   if (tile < -1 || tile >= NUM_TILES) return SVLA_EINVAL;
   g_force_tile = tile;
   return SVLA_OK;
+}
+
+int svla_gemm_tile_choice(int m, int n, int k, int act) {
+  if (m <= 0 || n <= 0 || k <= 0 || act < 0 || act > SVLA_ACT_SILU) return SVLA_EINVAL;
+  (void)act;  // the choice depends on the epilogue kind, not on the activation
+  return (int)pick_tile(m, n, k, EPI_STORE, true, n % 8 == 0).id;
 }
 
 int svla_gemm_set_split(int splits) {

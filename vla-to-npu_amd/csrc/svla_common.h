@@ -65,8 +65,9 @@ __device__ __forceinline__ float silu_f(float x) {
 __device__ __forceinline__ float gelu_tanh_f(float x) {
   // 2 * sqrt(2/pi) * log2(e) and 2 * sqrt(2/pi) * 0.044715 * log2(e)
   const float c0 = 2.3022082f, c1 = 0.10294324f;
-  const float z = x * __builtin_fmaf(c1, x * x, c0);
-  return x * fast_sigmoid_scaled(z);
+  // -z with the sign folded into the constants (exact)
+  const float nz = x * __builtin_fmaf(-c1, x * x, -c0);
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(nz));
 }
 
 // exact-erf GELU (the reference's nn.GELU() default)
