@@ -87,6 +87,8 @@ struct GemmArgs {
   // and one arrival counter per output tile (zero between calls)
   float* ws;
   unsigned* ws_cnt;
+  // persistent wide kernel: the tile grid (its launch grid is one workgroup per CU)
+  int tiles_m, tiles_n;
 };
 
 __device__ __forceinline__ long crow(const GemmArgs& p, int m) {
@@ -807,35 +809,51 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
       sA2[WBM * WBK], sA3[WBM * WBK];
   __shared__ __attribute__((aligned(1024))) bf16 sB0[WBN * WBK], sB1[WBN * WBK],
       sB2[WBN * WBK], sB3[WBN * WBK];
+  // epilogue staging, 8 KB per wave (32 rows x 128 columns), separate from the
+  // ring so the next tile's DMA can land while this tile is stored
+  __shared__ __attribute__((aligned(1024))) bf16 sOut[4][32 * 128];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int gn = gridDim.x;
-  const int tile = xcd_remap(blockIdx.y * gn + blockIdx.x, gn * gridDim.y);
-  int tm_idx, tn_idx;
-  tile_coords(tile, gridDim.y, gn, tm_idx, tn_idx);
-  const int m0 = tm_idx * WBM, n0 = tn_idx * WBN;
   const int nk = p.K / WBK;  // K % (4 * WBK) == 0 (checked by the launcher)
+  const int T = p.tiles_m * p.tiles_n, G = gridDim.x;
+  // workgroup b takes logical tiles slot(b), slot(b) + G, ...; slot() gives
+  // the workgroups of one XCD consecutive logical tiles, and tile_coords turns
+  // those into a compact patch of row and column blocks (shared panels in
+  // that XCD's L2)
+  int L = xcd_remap(blockIdx.x, G);
+  auto origin = [&](int l, int& m0_, int& n0_) __attribute__((always_inline)) {
+    int tm_idx, tn_idx;
+    tile_coords(l, p.tiles_m, p.tiles_n, tm_idx, tn_idx);
+    m0_ = tm_idx * WBM;
+    n0_ = tn_idx * WBN;
+  };
+  int m0, n0;
+  origin(L, m0, n0);
 
   // per-lane DMA sources: block b = wave * W_DMA + j covers rows 16b .. 16b+15;
   // lane -> row 16b + lane / 4, LDS slot lane % 4 holding logical chunk
   // pswz(row, slot).  Rows past M / N are clamped (their results are dropped).
   const bf16* a_src[W_DMA];
   const bf16* b_src[W_DMA];
+  auto set_src = [&](int m0_, int n0_) __attribute__((always_inline)) {
 #pragma unroll
-  for (int j = 0; j < W_DMA; ++j) {
-    const int r = (wave * W_DMA + j) * 16 + (lane >> 2);
-    const int g = pswz(r, lane & 3);
-    a_src[j] = p.a + (long)min(m0 + r, p.M - 1) * p.lda + g * 8;
-    b_src[j] = p.b + (long)min(n0 + r, p.N - 1) * p.ldb + g * 8;
-  }
+    for (int j = 0; j < W_DMA; ++j) {
+      const int r = (wave * W_DMA + j) * 16 + (lane >> 2);
+      const int g = pswz(r, lane & 3);
+      a_src[j] = p.a + (long)min(m0_ + r, p.M - 1) * p.lda + g * 8;
+      b_src[j] = p.b + (long)min(n0_ + r, p.N - 1) * p.ldb + g * 8;
+    }
+  };
+  set_src(m0, n0);
 
-  // DMA j of a stage: j < W_DMA -> A block, else B block j - W_DMA
+  // DMA j of a stage: j < W_DMA -> A block, else B block j - W_DMA; kt is a
+  // K tile of the tile whose sources are set
   auto issue_one = [&](auto SI, int j, int kt) __attribute__((always_inline)) {
     constexpr int S = decltype(SI)::value;
     bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
     bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
-    const int k = min(kt, nk - 1) * WBK;  // past the end: reload the last tile (never read)
+    const int k = kt * WBK;
     if (j < W_DMA)
       __builtin_amdgcn_global_load_lds((void*)(a_src[j] + k),
                                        (lds_ptr_t)(sa + (wave * W_DMA + j) * 512), 16, 0, 0);
@@ -843,16 +861,20 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
       __builtin_amdgcn_global_load_lds((void*)(b_src[j - W_DMA] + k),
                                        (lds_ptr_t)(sb + (wave * W_DMA + j - W_DMA) * 512), 16, 0, 0);
   };
-  auto issue = [&](auto SI, int kt) __attribute__((always_inline)) {
-#pragma unroll
-    for (int j = 0; j < 2 * W_DMA; ++j) issue_one(SI, j, kt);
-  };
 
   f32x4 acc[WTN][WTM];
+  auto zero_acc = [&]() __attribute__((always_inline)) {
 #pragma unroll
-  for (int i = 0; i < WTN; ++i)
+    for (int i = 0; i < WTN; ++i)
 #pragma unroll
-    for (int j = 0; j < WTM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < WTM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // zeroed accumulators are written by VALU; the first MFMA reads them as
+    // srcC.  The empty asm statements redefine every accumulator, and
+    // volatile asm keeps its order, so the zeroing cannot sink below the
+    // wait states.
+    pin_accumulators(acc);
+    asm volatile("s_nop 4");
+  };
 
   // fragment f of a stage: f < WTN -> weight tile f, else activation tile f - WTN
   const int fr = lane & 15, g = lane >> 4;
@@ -880,10 +902,14 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
 
   // One step of the ring: wait until stage s + 1 is in LDS for every wave and
   // every wave holds its stage-s fragments, then, between the first 32 of the
-  // 64 MFMAs of stage s: refill stage s's buffer with K tile s + 4 (one DMA
-  // every 4 MFMAs) and read stage s + 1's fragments into the other register
-  // set (one every 2 MFMAs), so the reads have landed by the next step.
-  auto step = [&](auto SI, auto SN, auto RC, int kt) __attribute__((always_inline)) {
+  // 64 MFMAs of stage s: refill stage s's buffer with K tile `next_kt` (one
+  // DMA every 4 MFMAs) and read stage s + 1's fragments into the other
+  // register set (one every 2 MFMAs), so the reads have landed by the next
+  // step.  (In vmcnt terms every VMEM instruction issued after a stage's DMA
+  // counts, stores included; the waits stay conservative.)
+  // (The last step of a tile reads nothing: the next tile's stage-0
+  // fragments are read after the epilogue, so they are not live across it.)
+  auto step = [&](auto SI, auto SN, auto RC, int next_kt, auto READ) __attribute__((always_inline)) {
     constexpr int R = decltype(RC)::value;
     using RN = std::integral_constant<int, 1 - R>;
     __builtin_amdgcn_s_waitcnt(kWaitStep);
@@ -891,137 +917,173 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < WTN * WTM; ++i) {
       mfma_agpr(acc[i / WTM][i % WTM], fw[R][i / WTM], fx[R][i % WTM]);
-      if (i < 32 && i % 4 == 0) issue_one(SI, i / 4, kt + 4);
-      if (i < 32 && i % 2 == 1) read_one(SN, RN{}, i / 2);
+      if (i < 32 && i % 4 == 0) issue_one(SI, i / 4, next_kt);
+      if constexpr (decltype(READ)::value)
+        if (i < 32 && i % 2 == 1) read_one(SN, RN{}, i / 2);
     }
   };
+  using RD = std::true_type;
+  using NR = std::false_type;
 
-  // zeroed accumulators are written by VALU; the first MFMA reads them as
-  // srcC.  The empty asm statements redefine every accumulator, and volatile
-  // asm keeps its order, so the zeroing cannot sink below the wait states.
-  pin_accumulators(acc);
-  asm volatile("s_nop 4");
-  issue(I0{}, 0);
-  issue(I1{}, 1);
-  issue(I2{}, 2);
-  issue(I3{}, 3);
+  // epilogue staging: row r (0 .. 31) of a wave's 32-row chunk is 32 slots of
+  // 4 columns; logical chunk c sits in slot c ^ ((r & 7) << 2)
+  bf16* const st = sOut[wave];
+  auto st_addr = [&](int r, int chunk) __attribute__((always_inline)) {
+    return st + r * 128 + ((chunk ^ ((r & 7) << 2)) << 2);
+  };
+
+  // prologue of the first tile
+#pragma unroll
+  for (int j = 0; j < 2 * W_DMA; ++j) issue_one(I0{}, j, 0);
+#pragma unroll
+  for (int j = 0; j < 2 * W_DMA; ++j) issue_one(I1{}, j, 1);
+#pragma unroll
+  for (int j = 0; j < 2 * W_DMA; ++j) issue_one(I2{}, j, 2);
+#pragma unroll
+  for (int j = 0; j < 2 * W_DMA; ++j) issue_one(I3{}, j, 3);
+  zero_acc();
   __builtin_amdgcn_s_waitcnt(kWaitPrologue);
   __builtin_amdgcn_s_barrier();
 #pragma unroll
   for (int f = 0; f < WTN + WTM; ++f) read_one(I0{}, I0{}, f);
-  for (int kt = 0; kt < nk; kt += 4) {  // nk % 4 == 0 (checked by the launcher)
-    step(I0{}, I1{}, I0{}, kt);
-    step(I1{}, I2{}, I1{}, kt + 1);
-    step(I2{}, I3{}, I0{}, kt + 2);
-    step(I3{}, I0{}, I1{}, kt + 3);
-  }
-  // drain the trailing (never read) DMA and fragment reads before exit, and
-  // let the last MFMAs retire before their accumulators are read
-  __builtin_amdgcn_s_waitcnt(0);
-  asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
-  // no accumulator read may be scheduled above the wait states
-  pin_accumulators(acc);
 
-  // ---- epilogue, staged through LDS so that every global store writes whole
-  // 128-byte lines.  In the MFMA layout a lane holds C[m][n .. n+3] for 16
-  // different rows per instruction, i.e. 32-byte pieces of 16 lines, which the
-  // memory side writes back as partial lines (measured: ~5x slower than
-  // line-sized stores and 1.3x the bytes).
-  // Phase 1 (MFMA layout): v = bf16(act(bf16(alpha * acc + bias))) goes to the
-  // wave's private 128 x 128 bf16 tile in LDS (the ring is free once every
-  // wave is past its last fragment read: the barrier below).  Row r of the
-  // tile is 32 chunks of 4 columns; chunk c sits in slot c ^ ((r & 7) << 2),
-  // so the 16 rows x 4 chunks of one write fall on distinct banks pairwise.
-  // Phase 2 (row layout): 16 lanes read a 256-byte row (one 16-byte read
-  // each, contiguous slots since the swizzle keeps bit 0), add the row-wise
-  // operands (position addend, residual) and store it with 16-byte stores.
-  __builtin_amdgcn_s_barrier();
-  bf16* st_lo = wave == 0 ? sA0 : wave == 1 ? sA2 : wave == 2 ? sB0 : sB2;  // rows 0 .. 63
-  bf16* st_hi = wave == 0 ? sA1 : wave == 1 ? sA3 : wave == 2 ? sB1 : sB3;  // rows 64 .. 127
-  auto st_addr = [&](int r, int chunk) __attribute__((always_inline)) {
-    return (r < 64 ? st_lo : st_hi) + (r & 63) * 128 + ((chunk ^ ((r & 7) << 2)) << 2);
-  };
-  const int wm0 = m0 + wm * 128, wn0 = n0 + wn * 128;
-  // per-column addend: bf16 bias + fp32 bias, summed once (fp32)
-  f32x4 cb[WTN];
-#pragma unroll
-  for (int tn = 0; tn < WTN; ++tn) cb[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (p.bias) {
-#pragma unroll
-    for (int tn = 0; tn < WTN; ++tn) {
-      const bf16x4 b4 = *reinterpret_cast<const bf16x4*>(p.bias + min(wn0 + tn * 16 + 4 * g, p.N - 4));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) cb[tn][i] = bf2f(b4[i]);
+  for (;;) {
+    const int wm0 = m0 + wm * 128, wn0 = n0 + wn * 128;
+    for (int kt = 0; kt + 4 < nk; kt += 4) {
+      step(I0{}, I1{}, I0{}, kt + 4, RD{});
+      step(I1{}, I2{}, I1{}, kt + 5, RD{});
+      step(I2{}, I3{}, I0{}, kt + 6, RD{});
+      step(I3{}, I0{}, I1{}, kt + 7, RD{});
     }
-  }
-  if (p.bias_f32) {
+    // per-column addend of the epilogue (bf16 bias + fp32 bias, summed once),
+    // loaded before the next tile's DMA so that waiting for it does not wait
+    // for that DMA
+    f32x4 cb[WTN];
 #pragma unroll
-    for (int tn = 0; tn < WTN; ++tn)
-      cb[tn] += *reinterpret_cast<const f32x4*>(p.bias_f32 + min(wn0 + tn * 16 + 4 * g, p.N - 4));
-  }
-  const float alpha = p.alpha;
+    for (int tn = 0; tn < WTN; ++tn) cb[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
 #pragma unroll
-  for (int tn = 0; tn < WTN; ++tn) {
+      for (int tn = 0; tn < WTN; ++tn) {
+        const bf16x4 b4 =
+            *reinterpret_cast<const bf16x4*>(p.bias + min(wn0 + tn * 16 + 4 * g, p.N - 4));
 #pragma unroll
-    for (int tm = 0; tm < WTM; ++tm) {
-      bf16x4 o;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = __builtin_fmaf(acc[tn][tm][i], alpha, cb[tn][i]);
-        if constexpr (ACT != SVLA_ACT_NONE) o[i] = f2bf(apply_act<ACT>(rbf(v)));
-        else o[i] = f2bf(v);
+        for (int i = 0; i < 4; ++i) cb[tn][i] = bf2f(b4[i]);
       }
-      *reinterpret_cast<bf16x4*>(st_addr(tm * 16 + fr, tn * 4 + g)) = o;
     }
-    // keep the next column tile's accumulator reads below this tile's LDS
-    // writes (otherwise the scheduler hoists all 256 AGPR reads up front and
-    // runs out of VGPRs)
-    if (tn + 1 < WTN) {
-      asm volatile("" ::: "memory");
+    if (p.bias_f32) {
 #pragma unroll
-      for (int tm = 0; tm < WTM; ++tm) asm volatile("" : "+a"(acc[tn + 1][tm]));
+      for (int tn = 0; tn < WTN; ++tn)
+        cb[tn] += *reinterpret_cast<const f32x4*>(p.bias_f32 + min(wn0 + tn * 16 + 4 * g, p.N - 4));
     }
-  }
-  // the same wave reads back what its lanes wrote (LDS operations of a wave
-  // complete in order)
-  constexpr int kRowsPerPass = 4, kPasses = 128 / kRowsPerPass, kBatch = 8;
-  const int j = lane & 15;
-  const int n = wn0 + 8 * j;
-#pragma unroll
-  for (int b0 = 0; b0 < kPasses; b0 += kBatch) {
-    bf16x8 v[kBatch], ad[kBatch], rs[kBatch];
-    int m[kBatch];
-#pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      const int r = (b0 + b) * kRowsPerPass + (lane >> 4);
-      m[b] = wm0 + r;
-      v[b] = *reinterpret_cast<const bf16x8*>(st_addr(r, 2 * j));
+    // last round: its DMA fetches the next tile's K tiles 0 .. 3 (or, after
+    // the last tile, reloads this tile's last K tile, never read); the wait
+    // of its last step has seen K tile 0 land for every wave
+    const int L_next = L + G;
+    const bool has_next = L_next < T;
+    int mn0 = m0, nn0 = n0;
+    if (has_next) {
+      origin(L_next, mn0, nn0);
+      set_src(mn0, nn0);
     }
-    if (p.rowadd) {
+    step(I0{}, I1{}, I0{}, has_next ? 0 : nk - 1, RD{});
+    step(I1{}, I2{}, I1{}, has_next ? 1 : nk - 1, RD{});
+    step(I2{}, I3{}, I0{}, has_next ? 2 : nk - 1, RD{});
+    step(I3{}, I0{}, I1{}, has_next ? 3 : nk - 1, NR{});
+    // let the last MFMAs retire before their accumulators are read
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+    pin_accumulators(acc);
+
+    // ---- epilogue, staged through LDS so that every global store writes
+    // whole 128-byte lines.  In the MFMA layout a lane holds C[m][n .. n+3]
+    // for 16 different rows per instruction, i.e. 32-byte pieces of 16
+    // lines, which the memory side writes back as partial lines (measured:
+    // ~5x slower than line-sized stores and 1.3x the bytes).  Per 32-row
+    // chunk of the wave tile:
+    //  phase 1 (MFMA layout): v = bf16(act(bf16(alpha * acc + addend))) into
+    //  the wave's staging buffer;
+    //  phase 2 (row layout): 16 lanes read a 256-byte row (one 16-byte read
+    //  each: the swizzle keeps bit 0, so slots 2j, 2j + 1 stay adjacent), add
+    //  the row-wise operands (position addend, residual) and store it.
+    // The staging buffer is private to the wave, whose LDS operations
+    // complete in order, so no barrier is needed.
+    const float alpha = p.alpha;
+    const int j = lane & 15;
+    const int ncol = wn0 + 8 * j;
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b)
-        ad[b] = ld8(p.rowadd + (long)(min(m[b], p.M - 1) % p.rowadd_period) * p.N + min(n, p.N - 8));
-    }
-    if (p.res) {
+    for (int c = 0; c < 4; ++c) {
 #pragma unroll
-      for (int b = 0; b < kBatch; ++b)
-        rs[b] = ld8(p.res + (long)min(m[b], p.M - 1) * p.ldr + min(n, p.N - 8));
-    }
+      for (int tn = 0; tn < WTN; ++tn) {
 #pragma unroll
-    for (int b = 0; b < kBatch; ++b) {
-      if (m[b] >= p.M || n >= p.N) continue;
-      bf16x8 o = v[b];
+        for (int h = 0; h < 2; ++h) {
+          const int tm = 2 * c + h;
+          bf16x4 o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float v = __builtin_fmaf(acc[tn][tm][i], alpha, cb[tn][i]);
+            if constexpr (ACT != SVLA_ACT_NONE) o[i] = f2bf(apply_act<ACT>(rbf(v)));
+            else o[i] = f2bf(v);
+          }
+          *reinterpret_cast<bf16x4*>(st_addr(h * 16 + fr, tn * 4 + g)) = o;
+        }
+      }
+      // keep the next chunk's accumulator reads below this chunk's LDS
+      // writes (otherwise the scheduler hoists all 256 AGPR reads up front
+      // and runs out of VGPRs)
+      if (c + 1 < 4) {
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int tn = 0; tn < WTN; ++tn) {
+          asm volatile("" : "+a"(acc[tn][2 * c + 2]));
+          asm volatile("" : "+a"(acc[tn][2 * c + 3]));
+        }
+      }
+#pragma unroll
+      for (int b0 = 0; b0 < 8; b0 += 4) {
+      bf16x8 v[4], ad[4], rs[4];
+      int m[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int r = (b0 + b) * 4 + (lane >> 4);
+        m[b] = wm0 + c * 32 + r;
+        v[b] = *reinterpret_cast<const bf16x8*>(st_addr(r, 2 * j));
+      }
       if (p.rowadd) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(ad[b][i]));
+        for (int b = 0; b < 4; ++b)
+          ad[b] = ld8(p.rowadd + (long)(min(m[b], p.M - 1) % p.rowadd_period) * p.N +
+                      min(ncol, p.N - 8));
       }
       if (p.res) {
 #pragma unroll
-        for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rs[b][i]));
+        for (int b = 0; b < 4; ++b)
+          rs[b] = ld8(p.res + (long)min(m[b], p.M - 1) * p.ldr + min(ncol, p.N - 8));
       }
-      st8(reinterpret_cast<bf16*>(p.c) + crow(p, m[b]) * p.ldc + n, o);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (m[b] >= p.M || ncol >= p.N) continue;
+        bf16x8 o = v[b];
+        if (p.rowadd) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(ad[b][i]));
+        }
+        if (p.res) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rs[b][i]));
+        }
+        st8(reinterpret_cast<bf16*>(p.c) + crow(p, m[b]) * p.ldc + ncol, o);
+      }
+      }
     }
+    if (!has_next) break;
+    L = L_next;
+    m0 = mn0;
+    n0 = nn0;
+    zero_acc();
+#pragma unroll
+    for (int f = 0; f < WTN + WTM; ++f) read_one(I0{}, I0{}, f);
   }
+  // drain the trailing (never read) DMA and the stores before exit
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
 // ---- skinny-M GEMM ----------------------------------------------------------
@@ -1475,6 +1537,11 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
   if (p.norm_w && p.K > 2048) return SVLA_EINVAL;  // row statistics keep <= 2048 per row
   const int gm = (p.M + t.bm - 1) / t.bm, gn = (p.N + t.bn - 1) / t.bn;
   dim3 grid(gn, gm, 1);
+  if (t.id == W256) {  // persistent: one workgroup per CU walks the tiles
+    p.tiles_m = gm;
+    p.tiles_n = gn;
+    grid = dim3(min(gm * gn, kNumCU), 1, 1);
+  }
   if (t.id == S32 || t.id == S64) {
     const int S = pick_split(gm * gn, p.K, t.bm, t.bn);
     const SplitWs* w = S > 1 ? split_ws(s) : nullptr;
