@@ -49,6 +49,18 @@ typedef void* svla_stream_t; /* hipStream_t */
 #define SVLA_MASK_CAUSAL 1
 #define SVLA_MASK_PREFIX_LM 2
 
+/* Harness elementwise operations (svla_unary_*). */
+#define SVLA_OP_SILU 0
+#define SVLA_OP_GELU_TANH 1
+#define SVLA_OP_GELU_ERF 2
+#define SVLA_OP_SIN 3
+#define SVLA_OP_COS 4
+
+/* Harness row norms (svla_row_norm). */
+#define SVLA_NORM_RMS 0     /* x * rsqrt(mean(x^2) + eps) * w                 (nn.RMSNorm) */
+#define SVLA_NORM_RMS_ADD 1 /* x / (||x|| / sqrt(cols) + eps) * w             (harness RMSNorm module) */
+#define SVLA_NORM_LAYER 2   /* (x - mean) / sqrt(var + eps) * w (+ b), biased var (LayerNorm) */
+
 /* Library version (major*10000 + minor*100 + patch). */
 int svla_version(void);
 
@@ -257,6 +269,49 @@ int svla_f32_to_bf16(const float* x, void* y, long n, svla_stream_t stream);
  * reference feeds random images straight in (vla/vla.py:306, 396-408). */
 int svla_image_to_bf16(const uint8_t* src, long src_bs, int n, int h, int w, void* dst,
                        int out_size, svla_stream_t stream);
+
+/* ------------------------------------------------------ harness kernels --
+ * The remaining per-kernel harness entry points, fp32 and bf16 variants
+ * (computed in fp32; bf16 results rounded where the matching torch reference
+ * rounds). */
+
+/* y = op(x) elementwise on n fp32 / bf16 values (op = SVLA_OP_*).  Replaces
+ * silu_float32 (cc/float/silu.cc), gelu (cc/float/gelu.cc,
+ * cc/bf16_new/gelu_bf16.cc), silu_bf16 / silu_bf16_small (cc/bf16_new/silu_bf16.cc),
+ * silu_{128,160}_float32 (cc/float/silu_128.cc, silu_160.cc), sin_float32 /
+ * cos_float32 (cc/float/sine.cc:64, cosine.cc:66) and sin_bfloat16 /
+ * cos_bfloat16 (cc/bf16_new/sine_bf16.cc, cosine_bf16.cc). */
+int svla_unary_f32(const float* x, float* y, long n, int op, svla_stream_t stream);
+int svla_unary_bf16(const void* x, void* y, long n, int op, svla_stream_t stream);
+
+/* out = x + y on n bf16 values.  Replaces add (cc/bf16_old/add_32_32_bf16.cc). */
+int svla_add_bf16(const void* x, const void* y, void* out, long n, svla_stream_t stream);
+
+/* Row norms with fp32 (is_f32 = 1: x, w, b, y all fp32) or bf16 I/O, kind =
+ * SVLA_NORM_*; b (LayerNorm only) may be NULL.  round_ops (bf16): round after
+ * every step a torch bf16 op chain rounds (the "new" harness references);
+ * otherwise round once.  cols <= 2048.  Replaces rms_norm (cc/float/rms_norm.cc,
+ * cc/bf16_new/rms_norm_bf16.cc), rms_norm_small, rms_norm_960 (cc/float/rms_norm_960.cc),
+ * layer_norm (cc/float/layer_norm.cc, cc/bf16_new/layer_norm_bf16.cc) and
+ * layer_norm_small. */
+int svla_row_norm(const void* x, int ldx, const void* w, const void* b, void* y, int ldy, int rows,
+                  int cols, float eps, int kind, int is_f32, int round_ops,
+                  svla_stream_t stream);
+
+/* Row softmax over cols, rows with strides lds / ldp; row_start >= 0 masks key
+ * c of row r when c > row_start + r / row_div (row_div > 1: several heads of
+ * one query row stored consecutively).  Replaces masked_softmax_float32
+ * (cc/float/masked_softmax.cc:72-127) and masked_softmax_128_float32
+ * (cc/float/masked_softmax_128.cc). */
+int svla_softmax_rows(const void* s, int lds, void* p, int ldp, int rows, int cols, int row_start,
+                      int row_div, int in_f32, int out_f32, svla_stream_t stream);
+
+/* fp32 Conv2d with kernel = stride = patch and no padding: images [n, C, H, W],
+ * kernel [E, C, patch, patch], bias [E] or NULL -> out [n * (H/patch) * (W/patch), E]
+ * (patches in row-major grid order).  Replaces conv (cc/float/conv.cc:12-55). */
+int svla_conv_patch_f32(const float* images, const float* kernel, const float* bias, float* out,
+                        int n_img, int chans, int height, int width, int patch, int embed,
+                        svla_stream_t stream);
 
 #ifdef __cplusplus
 }

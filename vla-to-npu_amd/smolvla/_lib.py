@@ -48,6 +48,12 @@ SIGNATURES = {
     "svla_time_embedding_bf16": [_d, _i, _d, _d, _p, _p],
     "svla_f32_to_bf16": [_p, _p, _l, _p],
     "svla_image_to_bf16": [_p, _l, _i, _i, _i, _p, _i, _p],
+    "svla_unary_f32": [_p, _p, _l, _i, _p],
+    "svla_unary_bf16": [_p, _p, _l, _i, _p],
+    "svla_add_bf16": [_p, _p, _p, _l, _p],
+    "svla_row_norm": [_p, _i, _p, _p, _p, _i, _i, _i, _f, _i, _i, _i, _p],
+    "svla_softmax_rows": [_p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p],
+    "svla_conv_patch_f32": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
 }
 
 RESTYPES = {}

@@ -15,6 +15,7 @@ import torch
 from . import ops
 
 BF16 = torch.bfloat16
+F32 = torch.float32
 
 
 def _into(dst, src):
@@ -115,3 +116,109 @@ def rope_fused_float32(x, sin_cos, out):
     s = sin_cos[:, :half].contiguous()
     c = sin_cos[:, half:].contiguous()
     ops.rope(x, 1, c, s, pos_offset=0, out=out)
+
+
+# ---- fp32 and "new" bf16 variants -----------------------------------------
+def _same(A, C):
+    if C.dtype != A.dtype or C.shape != A.shape:
+        raise ValueError("output must match the input's shape and dtype")
+
+
+def add(x, y, out):
+    """cc/bf16_old/add_32_32_bf16.cc (add/test_add.py: out = x + y, bf16)."""
+    ops.add(x, y, out=out)
+
+
+def silu_float32(A, C):
+    """cc/float/silu.cc (silu/test_silu.py: nn.SiLU in fp32)."""
+    _same(A, C)
+    ops.unary(A, "silu", out=C)
+
+
+silu_128_float32 = silu_float32  # cc/float/silu_128.cc (vla/tests/test_silu_128.py)
+silu_160_float32 = silu_float32  # cc/float/silu_160.cc (vla/tests/test_silu_160.py)
+
+
+def silu_bf16_small(A, C):
+    """cc/bf16_new/silu_bf16.cc small-tile entry (silu/test_silu_bf16_new.py:159-225)."""
+    _same(A, C)
+    ops.unary(A, "silu", out=C)
+
+
+def gelu(A, C):
+    """``gelu`` of cc/float/gelu.cc (fp32) and cc/bf16_new/gelu_bf16.cc (bf16):
+    nn.GELU() -- the exact erf form -- as gelu/test_gelu.py and
+    gelu/test_gelu_bf16_new.py compare against."""
+    _same(A, C)
+    ops.unary(A, "gelu_erf", out=C)
+
+
+gelu_small = gelu  # cc/bf16_new/gelu_bf16.cc small-tile entry (gelu/test_gelu_bf16_new.py:210)
+
+
+def sin_float32(A, C):
+    """cc/float/sine.cc:64 (sine/test_sine.py)."""
+    _same(A, C)
+    ops.unary(A, "sin", out=C)
+
+
+def cos_float32(A, C):
+    """cc/float/cosine.cc:66 (cosine/test_cosine.py)."""
+    _same(A, C)
+    ops.unary(A, "cos", out=C)
+
+
+sin_bfloat16 = sin_float32  # cc/bf16_new/sine_bf16.cc (sine/test_sine_bf16_new.py); dtype follows A
+cos_bfloat16 = cos_float32  # cc/bf16_new/cosine_bf16.cc (cosine/test_cosine_bf16.py)
+
+
+def rms_norm(A, B, C, eps=1e-6):
+    """``rms_norm`` of cc/float/rms_norm.cc and cc/bf16_new/rms_norm_bf16.cc:
+    the harness module y = x / (||x|| / sqrt(N) + eps) * w
+    (rms_norm/test_rms.py:25-33); bf16 rounds after every op like the torch
+    bf16 reference of rms_norm/test_rms_norm_bf16_new.py."""
+    ops.row_norm(A, B, eps, "rms_add", round_ops=A.dtype == BF16, out=C)
+
+
+rms_norm_small = rms_norm  # cc/bf16_new/rms_norm_bf16.cc small-tile entry
+
+
+def rms_norm_960(A, B, C, eps=1e-6):
+    """cc/float/rms_norm_960.cc (vla/tests/test_rms_norm_960.py): fp32, the
+    harness module y = x / (||x|| / sqrt(N) + eps) * w it is checked against
+    (:18-26)."""
+    ops.row_norm(A, B, eps, "rms_add", out=C)
+
+
+def layer_norm(A, B, C, bias=None, eps=1e-5):
+    """``layer_norm`` of cc/float/layer_norm.cc (gamma; the fp32 test adds the
+    beta separately, layer_norm/test_layer.py:56-80 -- here the optional
+    ``bias``) and cc/bf16_new/layer_norm_bf16.cc (gamma only, torch bf16 op
+    chain of layer_norm/test_layer_bf16_new.py:25-34)."""
+    ops.row_norm(A, B, eps, "layer", b=bias, round_ops=A.dtype == BF16, out=C)
+
+
+layer_norm_small = layer_norm  # cc/bf16_new/layer_norm_bf16.cc small-tile entry
+
+
+def masked_softmax_float32(scores, tile_row_start, weights, heads=1):
+    """cc/float/masked_softmax.cc:72-127: rows of ``heads`` consecutive
+    segments of keys (masked_softmax/test_masked_softmax.py: [64, 3 * 64]),
+    key c of row r masked when c > row_start + r."""
+    rs = int(tile_row_start.reshape(-1)[0].item()) if torch.is_tensor(tile_row_start) else int(
+        tile_row_start[0] if hasattr(tile_row_start, "__len__") else tile_row_start)
+    rows = scores.shape[0] * heads
+    cols = scores.numel() // rows
+    ops.softmax_rows(scores.reshape(rows, cols), rs, heads, out=weights.view(rows, cols))
+
+
+def masked_softmax_128_float32(scores, row_start, weights):
+    """cc/float/masked_softmax_128.cc (vla/tests/test_masked_softmax_128.py)."""
+    masked_softmax_float32(scores, row_start, weights, heads=1)
+
+
+def conv(images, kernel, out, bias=None):
+    """cc/float/conv.cc:12-55: fp32 patch convolution (kernel = stride = patch),
+    out [patches, E] (conv/test_conv.py)."""
+    ops.conv_patch_f32(images.reshape(-1, *images.shape[-3:]) if images.dim() == 4
+                       else images.unsqueeze(0), kernel, bias, out=out)

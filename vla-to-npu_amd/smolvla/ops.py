@@ -272,3 +272,71 @@ def image_to_bf16(frames, out_size=512, out=None):
     _lib.call("svla_image_to_bf16", _ptr(frames), h * w * 3, n, h, w, _ptr(out), out_size,
               _stream())
     return out
+
+
+# ------------------------------------------------------ harness variants ---
+UNARY = {"silu": 0, "gelu_tanh": 1, "gelu_erf": 2, "sin": 3, "cos": 4}
+NORM_KIND = {"rms": 0, "rms_add": 1, "layer": 2}
+
+
+def unary(x, op, out=None):
+    """Elementwise ``op`` (silu, gelu_tanh, gelu_erf, sin, cos) on a contiguous
+    fp32 or bf16 tensor, computed in fp32, same dtype out."""
+    if x.dtype not in (F32, BF16) or not x.is_contiguous():
+        raise ValueError("unary: contiguous fp32 or bf16 tensor expected")
+    out = torch.empty_like(x) if out is None else out
+    if out.dtype != x.dtype or not out.is_contiguous() or out.numel() != x.numel():
+        raise ValueError("unary: out must match x")
+    name = "svla_unary_f32" if x.dtype == F32 else "svla_unary_bf16"
+    _lib.call(name, _ptr(x), _ptr(out), x.numel(), UNARY[op], _stream())
+    return out
+
+
+def add(x, y, out=None):
+    """bf16 elementwise x + y (contiguous, same shape)."""
+    if x.dtype != BF16 or y.dtype != BF16 or x.shape != y.shape:
+        raise ValueError("add: two bf16 tensors of one shape expected")
+    x, y = x.contiguous(), y.contiguous()
+    out = torch.empty_like(x) if out is None else out
+    _lib.call("svla_add_bf16", _ptr(x), _ptr(y), _ptr(out), x.numel(), _stream())
+    return out
+
+
+def row_norm(x, w, eps, kind, b=None, round_ops=False, out=None):
+    """Row norm (kind rms / rms_add / layer) of a 2-D fp32 or bf16 tensor, all
+    operands of x's dtype."""
+    rows, cols = x.shape
+    out = torch.empty_like(x) if out is None else out
+    for t in (w, b, out):
+        if t is not None and t.dtype != x.dtype:
+            raise ValueError("row_norm: operands must share x's dtype")
+    _lib.call("svla_row_norm", _ptr(x), _ld(x), _ptr(w), _ptr(b), _ptr(out), _ld(out), rows,
+              cols, float(eps), NORM_KIND[kind], int(x.dtype == F32), int(round_ops), _stream())
+    return out
+
+
+def softmax_rows(s, row_start=-1, row_div=1, out=None, out_f32=None):
+    """Row softmax of a 2-D fp32 / bf16 view with the causal limit
+    ``c <= row_start + r // row_div`` (row_start < 0: unmasked)."""
+    rows, cols = s.shape
+    if out is None:
+        dt = (F32 if out_f32 else BF16) if out_f32 is not None else s.dtype
+        out = torch.empty(rows, cols, dtype=dt, device=s.device)
+    _lib.call("svla_softmax_rows", _ptr(s), _ld(s), _ptr(out), _ld(out), rows, cols,
+              int(row_start), int(row_div), int(s.dtype == F32), int(out.dtype == F32), _stream())
+    return out
+
+
+def conv_patch_f32(images, kernel, bias=None, out=None):
+    """fp32 Conv2d(k = stride = patch): images [n, C, H, W], kernel [E, C, P, P]
+    -> [n * (H/P) * (W/P), E]."""
+    n, c, h, w = images.shape
+    e, c2, pk, pk2 = kernel.shape
+    if c2 != c or pk != pk2 or images.dtype != F32 or kernel.dtype != F32:
+        raise ValueError("conv_patch_f32: fp32 images [n,C,H,W] and kernel [E,C,P,P] expected")
+    images, kernel = images.contiguous(), kernel.contiguous()
+    out = (torch.empty(n * (h // pk) * (w // pk), e, dtype=F32, device=images.device)
+           if out is None else out)
+    _lib.call("svla_conv_patch_f32", _ptr(images), _ptr(kernel), _ptr(bias), _ptr(out), n, c, h,
+              w, pk, e, _stream())
+    return out
