@@ -139,13 +139,19 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
     bf16* sv = S == 0 ? sV0 : S == 1 ? sV1 : sV2;
     blk = min(blk, nb - 1);  // past the end: reload the last block (never read)
     const int k0 = blk * BKEY;
-    const int rows_left = p.sk - 1 - k0;  // clamp rows into the tensor
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int key = (wave * 2 + j) * 8 + (lane >> 3);
-      const long adj = key > rows_left ? (long)(rows_left - key) : 0;
-      const bf16* gk = kb + (long)k0 * p.ldk + koff[j] + adj * p.ldk;
-      const bf16* gv = vb + (long)k0 * p.ldv + voff[j] + adj * p.ldv;
+      // block offsets are wave-uniform (scalar); only a partial last block
+      // (never in FULL) needs per-lane clamping of rows past sk
+      const bf16* gk = kb + (long)k0 * p.ldk + koff[j];
+      const bf16* gv = vb + (long)k0 * p.ldv + voff[j];
+      if constexpr (!FULL) {
+        const int key = (wave * 2 + j) * 8 + (lane >> 3);
+        const int rows_left = p.sk - 1 - k0;
+        const long adj = key > rows_left ? (long)(rows_left - key) : 0;
+        gk += adj * p.ldk;
+        gv += adj * p.ldv;
+      }
       __builtin_amdgcn_global_load_lds((void*)gk, (lds_ptr_t)(sk + (wave * 2 + j) * 512), 16, 0, 0);
       __builtin_amdgcn_global_load_lds((void*)gv, (lds_ptr_t)(sv + (wave * 2 + j) * 512), 16, 0, 0);
     }
@@ -215,10 +221,21 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[ts][qt][i]);
       mx = max_xor32(max_xor16(mx));
-      const float m_new = fmaxf(m_run[qt], mx);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;  // fully-masked-so-far guard
-      const float mc = m_use * c;
-      const float alpha = __builtin_amdgcn_exp2f(m_run[qt] * c - mc);
+      // Lazy rescaling: the running maximum moves only when some query of
+      // the wave sees a score more than 2^8 (in exp2 units) above it; until
+      // then the exponentials are taken against the stale maximum (values up
+      // to 256, rounded to bf16 with the same relative error as values <= 1)
+      // and the output / sum rescale is skipped for the whole wave.
+      const bool grow = mx * c > m_run[qt] * c + 8.f;  // false while everything is masked
+      if (__builtin_amdgcn_ballot_w64(grow)) {
+        const float m_new = fmaxf(m_run[qt], mx);
+        const float alpha = m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
+        l_run[qt] *= alpha;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[qt][t] *= alpha;
+        m_run[qt] = m_new;
+      }
+      const float mc = (m_run[qt] == -INFINITY ? 0.f : m_run[qt]) * c;  // fully-masked-so-far guard
       float psum = 0.f;
 #pragma unroll
       for (int ts = 0; ts < 4; ++ts)
@@ -229,10 +246,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
           pf[qt][ts >> 1][(ts & 1) * 4 + i] = f2bf(e);
         }
       psum = sum_xor32(sum_xor16(psum));
-      l_run[qt] = l_run[qt] * alpha + psum;
-      m_run[qt] = m_new;
-#pragma unroll
-      for (int t = 0; t < 4; ++t) o[qt][t] *= alpha;
+      l_run[qt] += psum;
     }
     // O^T[d, q] += V^T[d, keys] . P^T[keys, q]; V^T fragments shared by both query tiles
 #pragma unroll

@@ -802,6 +802,120 @@ __device__ __forceinline__ void pin_accumulators(f32x4 (&acc)[N1][N2]) {
     for (int j = 0; j < N2; ++j) asm volatile("" : "+a"(acc[i][j]));
 }
 
+// Per-column addend of the wide epilogue: bf16 bias + fp32 bias, summed once
+// (fp32), for the 8 MFMA column tiles of a 128-wide wave tile at column wn0.
+__device__ __forceinline__ void wide_addend(const GemmArgs& p, int wn0, int g, f32x4 (&cb)[WTN]) {
+#pragma unroll
+  for (int tn = 0; tn < WTN; ++tn) cb[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (p.bias) {
+#pragma unroll
+    for (int tn = 0; tn < WTN; ++tn) {
+      const bf16x4 b4 =
+          *reinterpret_cast<const bf16x4*>(p.bias + min(wn0 + tn * 16 + 4 * g, p.N - 4));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cb[tn][i] = bf2f(b4[i]);
+    }
+  }
+  if (p.bias_f32) {
+#pragma unroll
+    for (int tn = 0; tn < WTN; ++tn)
+      cb[tn] += *reinterpret_cast<const f32x4*>(p.bias_f32 + min(wn0 + tn * 16 + 4 * g, p.N - 4));
+  }
+}
+
+// Epilogue of a 128 x 128 wave tile (accumulators in AGPRs, MFMA layout),
+// staged through LDS so that every global store writes whole 128-byte lines.
+// In the MFMA layout a lane holds C[m][n .. n+3] for 16 different rows per
+// instruction, i.e. 32-byte pieces of 16 lines, which the memory side writes
+// back as partial lines (measured: ~5x slower than line-sized stores and 1.3x
+// the bytes).  Per 32-row chunk of the wave tile:
+//  phase 1 (MFMA layout): v = bf16(act(bf16(alpha * acc + addend))) into the
+//  wave's 8 KB staging buffer `st` (row r: 32 slots of 4 columns, chunk c in
+//  slot c ^ ((r & 7) << 2), so the 16 rows x 4 chunks of one write fall on
+//  distinct banks pairwise);
+//  phase 2 (row layout): 16 lanes read a 256-byte row (one 16-byte read each:
+//  the swizzle keeps bit 0, so slots 2j, 2j + 1 stay adjacent), add the
+//  row-wise operands (position addend, residual) and store it.
+// The staging buffer is private to the wave, whose LDS operations complete
+// in order, so no barrier is needed.
+template <int ACT>
+__device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WTN][WTM],
+                                              const f32x4 (&cb)[WTN], bf16* st, int wm0,
+                                              int wn0, int lane) {
+  const int fr = lane & 15, g = lane >> 4;
+  auto st_addr = [&](int r, int chunk) __attribute__((always_inline)) {
+    return st + r * 128 + ((chunk ^ ((r & 7) << 2)) << 2);
+  };
+  const float alpha = p.alpha;
+  const int j = lane & 15;
+  const int ncol = wn0 + 8 * j;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+#pragma unroll
+    for (int tn = 0; tn < WTN; ++tn) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int tm = 2 * c + h;
+        bf16x4 o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = __builtin_fmaf(acc[tn][tm][i], alpha, cb[tn][i]);
+          if constexpr (ACT != SVLA_ACT_NONE) o[i] = f2bf(apply_act<ACT>(rbf(v)));
+          else o[i] = f2bf(v);
+        }
+        *reinterpret_cast<bf16x4*>(st_addr(h * 16 + fr, tn * 4 + g)) = o;
+      }
+    }
+    // keep the next chunk's accumulator reads below this chunk's LDS writes
+    // (otherwise the scheduler hoists all 256 AGPR reads up front and runs
+    // out of VGPRs)
+    if (c + 1 < 4) {
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int tn = 0; tn < WTN; ++tn) {
+        asm volatile("" : "+a"(acc[tn][2 * c + 2]));
+        asm volatile("" : "+a"(acc[tn][2 * c + 3]));
+      }
+    }
+#pragma unroll
+    for (int b0 = 0; b0 < 8; b0 += 4) {
+      bf16x8 v[4], ad[4], rs[4];
+      int m[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int r = (b0 + b) * 4 + (lane >> 4);
+        m[b] = wm0 + c * 32 + r;
+        v[b] = *reinterpret_cast<const bf16x8*>(st_addr(r, 2 * j));
+      }
+      if (p.rowadd) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          ad[b] = ld8(p.rowadd + (long)(min(m[b], p.M - 1) % p.rowadd_period) * p.N +
+                      min(ncol, p.N - 8));
+      }
+      if (p.res) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b)
+          rs[b] = ld8(p.res + (long)min(m[b], p.M - 1) * p.ldr + min(ncol, p.N - 8));
+      }
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        if (m[b] >= p.M || ncol >= p.N) continue;
+        bf16x8 o = v[b];
+        if (p.rowadd) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(ad[b][i]));
+        }
+        if (p.res) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rs[b][i]));
+        }
+        st8(reinterpret_cast<bf16*>(p.c) + crow(p, m[b]) * p.ldc + ncol, o);
+      }
+    }
+  }
+}
+
 template <int AMODE, bool NORM, int EPI, int ACT>
 __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   static_assert(AMODE == A_DENSE && !NORM && EPI == EPI_STORE, "wide tile: plain dense GEMM");
@@ -925,12 +1039,6 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   using RD = std::true_type;
   using NR = std::false_type;
 
-  // epilogue staging: row r (0 .. 31) of a wave's 32-row chunk is 32 slots of
-  // 4 columns; logical chunk c sits in slot c ^ ((r & 7) << 2)
-  bf16* const st = sOut[wave];
-  auto st_addr = [&](int r, int chunk) __attribute__((always_inline)) {
-    return st + r * 128 + ((chunk ^ ((r & 7) << 2)) << 2);
-  };
 
   // prologue of the first tile
 #pragma unroll
@@ -959,22 +1067,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
     // loaded before the next tile's DMA so that waiting for it does not wait
     // for that DMA
     f32x4 cb[WTN];
-#pragma unroll
-    for (int tn = 0; tn < WTN; ++tn) cb[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (p.bias) {
-#pragma unroll
-      for (int tn = 0; tn < WTN; ++tn) {
-        const bf16x4 b4 =
-            *reinterpret_cast<const bf16x4*>(p.bias + min(wn0 + tn * 16 + 4 * g, p.N - 4));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) cb[tn][i] = bf2f(b4[i]);
-      }
-    }
-    if (p.bias_f32) {
-#pragma unroll
-      for (int tn = 0; tn < WTN; ++tn)
-        cb[tn] += *reinterpret_cast<const f32x4*>(p.bias_f32 + min(wn0 + tn * 16 + 4 * g, p.N - 4));
-    }
+    wide_addend(p, wn0, g, cb);
     // last round: its DMA fetches the next tile's K tiles 0 .. 3 (or, after
     // the last tile, reloads this tile's last K tile, never read); the wait
     // of its last step has seen K tile 0 land for every wave
@@ -993,87 +1086,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
     pin_accumulators(acc);
 
-    // ---- epilogue, staged through LDS so that every global store writes
-    // whole 128-byte lines.  In the MFMA layout a lane holds C[m][n .. n+3]
-    // for 16 different rows per instruction, i.e. 32-byte pieces of 16
-    // lines, which the memory side writes back as partial lines (measured:
-    // ~5x slower than line-sized stores and 1.3x the bytes).  Per 32-row
-    // chunk of the wave tile:
-    //  phase 1 (MFMA layout): v = bf16(act(bf16(alpha * acc + addend))) into
-    //  the wave's staging buffer;
-    //  phase 2 (row layout): 16 lanes read a 256-byte row (one 16-byte read
-    //  each: the swizzle keeps bit 0, so slots 2j, 2j + 1 stay adjacent), add
-    //  the row-wise operands (position addend, residual) and store it.
-    // The staging buffer is private to the wave, whose LDS operations
-    // complete in order, so no barrier is needed.
-    const float alpha = p.alpha;
-    const int j = lane & 15;
-    const int ncol = wn0 + 8 * j;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-#pragma unroll
-      for (int tn = 0; tn < WTN; ++tn) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const int tm = 2 * c + h;
-          bf16x4 o;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const float v = __builtin_fmaf(acc[tn][tm][i], alpha, cb[tn][i]);
-            if constexpr (ACT != SVLA_ACT_NONE) o[i] = f2bf(apply_act<ACT>(rbf(v)));
-            else o[i] = f2bf(v);
-          }
-          *reinterpret_cast<bf16x4*>(st_addr(h * 16 + fr, tn * 4 + g)) = o;
-        }
-      }
-      // keep the next chunk's accumulator reads below this chunk's LDS
-      // writes (otherwise the scheduler hoists all 256 AGPR reads up front
-      // and runs out of VGPRs)
-      if (c + 1 < 4) {
-        asm volatile("" ::: "memory");
-#pragma unroll
-        for (int tn = 0; tn < WTN; ++tn) {
-          asm volatile("" : "+a"(acc[tn][2 * c + 2]));
-          asm volatile("" : "+a"(acc[tn][2 * c + 3]));
-        }
-      }
-#pragma unroll
-      for (int b0 = 0; b0 < 8; b0 += 4) {
-      bf16x8 v[4], ad[4], rs[4];
-      int m[4];
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int r = (b0 + b) * 4 + (lane >> 4);
-        m[b] = wm0 + c * 32 + r;
-        v[b] = *reinterpret_cast<const bf16x8*>(st_addr(r, 2 * j));
-      }
-      if (p.rowadd) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          ad[b] = ld8(p.rowadd + (long)(min(m[b], p.M - 1) % p.rowadd_period) * p.N +
-                      min(ncol, p.N - 8));
-      }
-      if (p.res) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          rs[b] = ld8(p.res + (long)min(m[b], p.M - 1) * p.ldr + min(ncol, p.N - 8));
-      }
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        if (m[b] >= p.M || ncol >= p.N) continue;
-        bf16x8 o = v[b];
-        if (p.rowadd) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(ad[b][i]));
-        }
-        if (p.res) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rs[b][i]));
-        }
-        st8(reinterpret_cast<bf16*>(p.c) + crow(p, m[b]) * p.ldc + ncol, o);
-      }
-      }
-    }
+    wide_epilogue<ACT>(p, acc, cb, sOut[wave], wm0, wn0, lane);
     if (!has_next) break;
     L = L_next;
     m0 = mn0;
