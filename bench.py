@@ -80,25 +80,44 @@ def time_chunks(eng, n):
     return out
 
 
+def _up_proj_launcher(cfg, M, x, w_packed, bias, wide):
+    """The ViT MLP up-projection exactly as the engine launches it at this
+    row count: on the 256x256 kernel with slab-blocked weights and a
+    slab-blocked output when ``wide`` (``layers.vit_wide_ok``), else through
+    ``ops.linear``."""
+    from smolvla import ops
+    v = cfg.vit
+    if wide:
+        wb = ops.slab_block(w_packed)
+        out = torch.empty(v.inter // 32, M, 32, device="cuda", dtype=torch.bfloat16)
+        lay = ops.LAYOUT_W_BLOCKED | ops.LAYOUT_C_BLOCKED
+        return lambda: ops.linear_wide(x, wb, M, v.inter, v.hidden, bias=bias,
+                                       act="gelu_" + v.gelu, out=out, layout=lay)
+    out = torch.empty(M, v.inter, device="cuda", dtype=torch.bfloat16)
+    return lambda: ops.linear(x, w_packed, bias=bias, act="gelu_" + v.gelu, out=out)
+
+
 def dominant_kernel_roofline(eng, iters):
     """The ViT MLP up-projection (GEMM 96k x 3072 x 768 at batch 32 with the
-    bias + tanh-GELU epilogue; the only GEMM instantiated with GELU).  Launched
-    `iters` times back-to-back on the current stream between two HIP events."""
-    from smolvla import ops
+    bias + tanh-GELU epilogue; the only GEMM instantiated with GELU), launched
+    as the engine launches it, `iters` times back-to-back on the current
+    stream between two HIP events."""
+    from smolvla import layers
     cfg = eng.cfg
     v = cfg.vit
     P = eng.vit[0]
     M = eng.vit_x.shape[0]
     x = eng.vbufs.get("vh", M, v.hidden)
-    out = eng.vbufs.get("vmlp", M, v.inter)
+    wide = layers.vit_wide_ok(v, M)
+    run = _up_proj_launcher(cfg, M, x, P["wup"], P["bup"], wide)
     for _ in range(3):
-        ops.linear(x, P["wup"], bias=P["bup"], act="gelu_" + v.gelu, out=out)
+        run()
     torch.cuda.synchronize()
     a = torch.cuda.Event(enable_timing=True)
     b = torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(iters):
-        ops.linear(x, P["wup"], bias=P["bup"], act="gelu_" + v.gelu, out=out)
+        run()
     b.record()
     b.synchronize()
     avg_ms = a.elapsed_time(b) / iters
@@ -109,8 +128,9 @@ def dominant_kernel_roofline(eng, iters):
     traffic = tr.get("bytes_per_launch") if tr and tr.get("shape") == [M, v.inter, v.hidden] else None
     from smolvla import _lib
     tile = _lib.load().svla_gemm_tile_choice(M, v.inter, v.hidden, 1)
-    kname = {8: "gemm_wide_kernel<0, false, 0, 1> (256x256 tile, 4-stage LDS-DMA ring, "
-                "LDS-staged bias + tanh-GELU epilogue)",
+    kname = {8: "gemm_wide_kernel<0, false, 0, 1> (persistent 256x256 tile, 4-stage LDS-DMA ring, "
+                "LDS-staged bias + tanh-GELU epilogue" +
+                (", slab-blocked weights and output)" if wide else ")"),
              7: "gemm_pipe_kernel<128, 128, 0, false, 0, 1> (128x128 LDS-DMA pipeline, "
                 "bias + tanh-GELU epilogue)"}.get(tile, f"GEMM tile configuration {tile}")
     return {
@@ -138,9 +158,11 @@ def traffic_probe(cfg, batch):
     x = torch.randn(M, v.hidden, device="cuda", generator=g).to(torch.bfloat16)
     w = (torch.randn(v.inter, v.hidden, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
     b = (torch.randn(v.inter, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
-    out = torch.empty(M, v.inter, device="cuda", dtype=torch.bfloat16)
+    from smolvla import layers
+    run = _up_proj_launcher(cfg, M, x, w, b, layers.vit_wide_ok(v, M))
+    torch.cuda.synchronize()
     for _ in range(3):
-        ops.linear(x, w, bias=b, act="gelu_" + v.gelu, out=out)
+        run()
     src = torch.ones(1 << 29, device="cuda", dtype=torch.bfloat16)   # 1 GiB
     dst = torch.empty_like(src)
     for _ in range(3):

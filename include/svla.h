@@ -49,6 +49,12 @@ typedef void* svla_stream_t; /* hipStream_t */
 #define SVLA_MASK_CAUSAL 1
 #define SVLA_MASK_PREFIX_LM 2
 
+/* Layout flags of svla_linear_wide_bf16: slab-blocked A, W or C.  A blocked
+ * [rows, K] matrix stores element (r, k) at (k / 32) * rows * 32 + r * 32 + k % 32. */
+#define SVLA_LAYOUT_A_BLOCKED 1
+#define SVLA_LAYOUT_W_BLOCKED 2
+#define SVLA_LAYOUT_C_BLOCKED 4
+
 /* Harness elementwise operations (svla_unary_*). */
 #define SVLA_OP_SILU 0
 #define SVLA_OP_GELU_TANH 1
@@ -104,6 +110,23 @@ int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void*
                      const float* bias_f32, const void* res, int ldr, void* c, int ldc, int m,
                      int n, int k, float alpha, int act, int out_f32, const void* norm_w,
                      float norm_eps, svla_stream_t stream);
+
+/* The big-problem GEMM of svla_linear_bf16 (persistent 256x256 tiles, plain
+ * store epilogue: bias, fp32 bias, alpha, activation, residual) with optional
+ * slab-blocked layouts (SVLA_LAYOUT_*): a slab-blocked operand streams into
+ * LDS as contiguous kilobytes (measured on MI355X: ~41 B/clk/CU against
+ * ~22 for the 64-byte row pieces of the row-major layout).  lda / ldw / ldc
+ * are ignored for blocked matrices.  m % 256 == 0, n % 256 == 0,
+ * k % 128 == 0; res (row-major) only with a row-major C.  Same numerics as
+ * svla_linear_bf16.  Replaces the same reference GEMMs (the ViT projections,
+ * vla/vision_block_bf16.py:135-169). */
+int svla_linear_wide_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
+                          const float* bias_f32, const void* res, int ldr, void* c, int ldc, int m,
+                          int n, int k, float alpha, int act, int layout, svla_stream_t stream);
+
+/* Row-major [rows, k] (leading dimension ldx) -> slab-blocked [k/32][rows][32]
+ * (for weights and inputs of svla_linear_wide_bf16).  k % 32 == 0. */
+int svla_slab_block_bf16(const void* x, int ldx, void* out, int rows, int k, svla_stream_t stream);
 
 /* Tuning hook: force the GEMM tile configuration for every later call
  * (0: 256x256/32x32-MFMA, 1: 128x128/32x32, 2: 64x128/16x16, 3: 64x64/16x16,

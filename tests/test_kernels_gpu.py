@@ -156,6 +156,51 @@ def test_wide_tile_forced(ops, force_tile, M, N, K):
     assert rel_err(got, a.float() @ w.float() + bf) < 1e-3
 
 
+def test_slab_block_roundtrip(ops):
+    g = gen(40)
+    x = randn(g, 300, 96).cuda()
+    xb = ops.slab_block(x)
+    assert xb.shape == (3, 300, 32)
+    assert torch.equal(ops.unblock(xb), x)
+    assert torch.equal(xb[1, 7], x[7, 32:64])
+
+
+@pytest.mark.parametrize("layout", range(8))
+def test_linear_wide_layouts(ops, force_tile, layout):
+    """svla_linear_wide_bf16 with every combination of slab-blocked A, W and C
+    gives bit-for-bit the row-major result of the same (forced) kernel: bias +
+    GELU, and bias + residual when C is row-major."""
+    g = gen(41 + layout)
+    M, N, K = 512, 768, 384
+    a, w, b = randn(g, M, K).cuda(), randn(g, K, N, std=0.05).cuda(), randn(g, N, std=0.05).cuda()
+    wp = ops.pack_weight(w)
+    force_tile(8)
+    want = ops.linear(a, wp, bias=b, act="gelu_tanh")
+    res = randn(g, M, N).cuda()
+    want_res = ops.linear(a, wp, bias=b, res=res)
+    force_tile(-1)
+    A = ops.slab_block(a) if layout & ops.LAYOUT_A_BLOCKED else a
+    W = ops.slab_block(wp) if layout & ops.LAYOUT_W_BLOCKED else wp
+    got = ops.linear_wide(A, W, M, N, K, bias=b, act="gelu_tanh", layout=layout)
+    if layout & ops.LAYOUT_C_BLOCKED:
+        got = ops.unblock(got)
+    assert torch.equal(got, want)
+    if not layout & ops.LAYOUT_C_BLOCKED:
+        got = ops.linear_wide(A, W, M, N, K, bias=b, res=res, layout=layout)
+        assert torch.equal(got, want_res)
+    assert_close_bf16(want, ref.gelu(ref.linear(a.cpu(), w.cpu(), b.cpu()), "tanh"))
+
+
+def test_linear_wide_rejects_bad_shapes(ops):
+    a = torch.zeros(300, 384, dtype=BF16, device="cuda")
+    w = torch.zeros(768, 384, dtype=BF16, device="cuda")
+    from smolvla._lib import SvlaError
+    with pytest.raises(SvlaError):
+        ops.linear_wide(a, w, 300, 768, 384)        # M % 256 != 0
+    with pytest.raises(SvlaError):
+        ops.linear_wide(a[:256], w[:700], 256, 700, 384)  # N % 256 != 0
+
+
 def test_wide_tile_auto_vit_up(ops):
     # a ViT MLP up-projection large enough for the automatic wide-tile choice
     g = gen(17)

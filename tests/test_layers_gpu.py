@@ -195,3 +195,29 @@ def test_joint_transformer_two_layers():
     v2, k2, vv2 = ref.decoder_block(v1, pv, V)
     want = ref.expert_cross_block(a, k2, vv2, pc, E)
     check(got, want[0])
+
+
+@pytest.mark.parametrize("biases", [True, False])
+def test_vit_layer_wide_blocked(biases):
+    """The ViT block on the 256x256 GEMM with slab-blocked weights and a
+    slab-blocked MLP activation (the batch-32 engine's path) against the
+    oracle, and bit-identical to the row-major path forced onto the same
+    kernel."""
+    from smolvla import _lib, layers
+    cfg = VitConfig()
+    p = vit_layer_params(_Gen(124, norm_init="random"), cfg, biases=biases)
+    x = x_in(125, 2, 1024, 768)
+    want = ref.vit_block(x, p, cfg)
+    P = layers.prep_vit(p, "cuda", wide=True)
+    xg = x.reshape(2048, 768).cuda()
+    layers.vit_layer(xg, P, cfg, 2, 1024)
+    check(xg.view(2, 1024, 768), want)
+    lib = _lib.load()
+    lib.svla_gemm_set_tile(8)
+    try:
+        Pr = dict(P, wide=False)
+        xr = x.reshape(2048, 768).cuda()
+        layers.vit_layer(xr, Pr, cfg, 2, 1024)
+    finally:
+        lib.svla_gemm_set_tile(-1)
+    assert torch.equal(xr, xg)

@@ -89,6 +89,11 @@ struct GemmArgs {
   unsigned* ws_cnt;
   // persistent wide kernel: the tile grid (its launch grid is one workgroup per CU)
   int tiles_m, tiles_n;
+  // slab-blocked operands / output of the wide kernel: element (row, k) of a
+  // blocked [rows, K] matrix sits at (k / 32) * rows * 32 + row * 32 + k % 32,
+  // so the 16 rows x 32 columns an LDS-DMA instruction fetches are one
+  // contiguous kilobyte (the row-major layout gives 16 separate 64-byte pieces)
+  int a_blk, b_blk, c_blk;
 };
 
 __device__ __forceinline__ long crow(const GemmArgs& p, int m) {
@@ -910,7 +915,10 @@ __device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WT
 #pragma unroll
           for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rs[b][i]));
         }
-        st8(reinterpret_cast<bf16*>(p.c) + crow(p, m[b]) * p.ldc + ncol, o);
+        bf16* dst = p.c_blk ? reinterpret_cast<bf16*>(p.c) + (long)(ncol >> 5) * p.M * WBK +
+                                  (long)m[b] * WBK + (ncol & 31)
+                            : reinterpret_cast<bf16*>(p.c) + crow(p, m[b]) * p.ldc + ncol;
+        st8(dst, o);
       }
     }
   }
@@ -948,6 +956,9 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   // per-lane DMA sources: block b = wave * W_DMA + j covers rows 16b .. 16b+15;
   // lane -> row 16b + lane / 4, LDS slot lane % 4 holding logical chunk
   // pswz(row, slot).  Rows past M / N are clamped (their results are dropped).
+  // row and K-step strides of A and W (elements): row-major, or slab-blocked
+  const long a_rs = p.a_blk ? WBK : p.lda, a_ks = p.a_blk ? (long)p.M * WBK : WBK;
+  const long b_rs = p.b_blk ? WBK : p.ldb, b_ks = p.b_blk ? (long)p.N * WBK : WBK;
   const bf16* a_src[W_DMA];
   const bf16* b_src[W_DMA];
   auto set_src = [&](int m0_, int n0_) __attribute__((always_inline)) {
@@ -955,8 +966,8 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
     for (int j = 0; j < W_DMA; ++j) {
       const int r = (wave * W_DMA + j) * 16 + (lane >> 2);
       const int g = pswz(r, lane & 3);
-      a_src[j] = p.a + (long)min(m0_ + r, p.M - 1) * p.lda + g * 8;
-      b_src[j] = p.b + (long)min(n0_ + r, p.N - 1) * p.ldb + g * 8;
+      a_src[j] = p.a + (long)min(m0_ + r, p.M - 1) * a_rs + g * 8;
+      b_src[j] = p.b + (long)min(n0_ + r, p.N - 1) * b_rs + g * 8;
     }
   };
   set_src(m0, n0);
@@ -967,12 +978,11 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
     constexpr int S = decltype(SI)::value;
     bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
     bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
-    const int k = kt * WBK;
     if (j < W_DMA)
-      __builtin_amdgcn_global_load_lds((void*)(a_src[j] + k),
+      __builtin_amdgcn_global_load_lds((void*)(a_src[j] + kt * a_ks),
                                        (lds_ptr_t)(sa + (wave * W_DMA + j) * 512), 16, 0, 0);
     else
-      __builtin_amdgcn_global_load_lds((void*)(b_src[j - W_DMA] + k),
+      __builtin_amdgcn_global_load_lds((void*)(b_src[j - W_DMA] + kt * b_ks),
                                        (lds_ptr_t)(sb + (wave * W_DMA + j - W_DMA) * 512), 16, 0, 0);
   };
 
@@ -1350,6 +1360,20 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
   }
 }
 
+// Row-major [rows, k] (leading dimension ldx) -> slab-blocked [k / 32][rows][32]:
+// one thread per 16-byte piece, reading along rows and writing along slabs.
+__global__ __launch_bounds__(256) void slab_block_kernel(const bf16* __restrict__ x, long ldx,
+                                                         bf16* __restrict__ out, int rows, int k) {
+  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;  // piece index, slab-major
+  const int per_slab_row = WBK / 8;
+  const long per_slab = (long)rows * per_slab_row;
+  if (i >= per_slab * (k / WBK)) return;
+  const int slab = (int)(i / per_slab);
+  const long rem = i - (long)slab * per_slab;
+  const int r = (int)(rem / per_slab_row), q = (int)(rem - (long)r * per_slab_row);
+  st8(out + i * 8, ld8(x + (long)r * ldx + slab * WBK + q * 8));
+}
+
 // ---- launch ---------------------------------------------------------------
 enum TileId { T256 = 0, T128 = 1, T64x128 = 2, T64 = 3, S64 = 4, S32 = 5, T128S = 6,
               P128 = 7, W256 = 8, P64 = 9, NUM_TILES = 10 };
@@ -1627,6 +1651,44 @@ int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void*
   p.norm_w = static_cast<const bf16*>(norm_w);
   p.norm_eps = norm_eps;
   return run_gemm<A_DENSE>(p, EPI_STORE, act, (hipStream_t)stream);
+}
+
+int svla_linear_wide_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
+                          const float* bias_f32, const void* res, int ldr, void* c, int ldc, int m,
+                          int n, int k, float alpha, int act, int layout, svla_stream_t stream) {
+  if (act < 0 || act > SVLA_ACT_SILU || (layout & ~7)) return SVLA_EINVAL;
+  if (m <= 0 || m % WBM || n % WBN || k % (4 * WBK)) return SVLA_EINVAL;
+  if ((long)m * k > (1L << 31) || (long)n * k > (1L << 31)) return SVLA_EINVAL;
+  if (bias_f32 && !svla_aligned16(bias_f32)) return SVLA_EINVAL;
+  if (res && ((layout & SVLA_LAYOUT_C_BLOCKED) || ldr % 8 || !svla_aligned16(res))) return SVLA_EINVAL;
+  GemmArgs p = base_args(a, (layout & SVLA_LAYOUT_A_BLOCKED) ? k : lda, w,
+                         (layout & SVLA_LAYOUT_W_BLOCKED) ? k : ldw, c,
+                         (layout & SVLA_LAYOUT_C_BLOCKED) ? n : ldc, m, n, k);
+  if (p.lda % 8 || p.ldb % 8 || p.ldc % 8 || !svla_aligned16(a) || !svla_aligned16(w) ||
+      !svla_aligned16(c))
+    return SVLA_EINVAL;
+  p.alpha = alpha;
+  p.bias = static_cast<const bf16*>(bias);
+  p.bias_f32 = bias_f32;
+  p.res = static_cast<const bf16*>(res);
+  p.ldr = ldr;
+  p.a_blk = (layout & SVLA_LAYOUT_A_BLOCKED) != 0;
+  p.b_blk = (layout & SVLA_LAYOUT_W_BLOCKED) != 0;
+  p.c_blk = (layout & SVLA_LAYOUT_C_BLOCKED) != 0;
+  p.tiles_m = m / WBM;
+  p.tiles_n = n / WBN;
+  const dim3 grid(min(p.tiles_m * p.tiles_n, kNumCU), 1, 1);
+  return dispatch<A_DENSE, false>(p, EPI_STORE, act, W256, grid, (hipStream_t)stream);
+}
+
+int svla_slab_block_bf16(const void* x, int ldx, void* out, int rows, int k, svla_stream_t stream) {
+  if (rows <= 0 || k <= 0 || k % WBK || ldx < k) return SVLA_EINVAL;
+  const long total = (long)rows * k / 8;  // 16-byte pieces
+  hipLaunchKernelGGL(slab_block_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<const bf16*>(x), (long)ldx,
+                     static_cast<bf16*>(out), rows, k);
+  SVLA_CHECK_LAUNCH();
+  return SVLA_OK;
 }
 
 int svla_linear_rope_bf16(const void* a, int lda, const void* w, int ldw, void* c, int ldc,

@@ -26,6 +26,8 @@ SIGNATURES = {
     "svla_gemm_set_tile": [_i],
     "svla_gemm_set_split": [_i],
     "svla_gemm_tile_choice": [_i, _i, _i, _i],
+    "svla_linear_wide_bf16": [_p, _i, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _i, _i, _p],
+    "svla_slab_block_bf16": [_p, _i, _p, _i, _i, _p],
     "svla_linear_bf16": [_p, _i, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _i, _i, _p, _f,
                          _p],
     "svla_linear_rope_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _f, _p],

@@ -70,7 +70,10 @@ def prep_cross(p, device):
     )
 
 
-def prep_vit(p, device):
+def prep_vit(p, device, wide=False):
+    """Packed ViT block weights.  ``wide``: also slab-blocked copies for the
+    256x256 GEMM (``ops.linear_wide``), used when every ViT projection at the
+    engine's row count runs on that kernel."""
     H = p["Wq"].shape[0]
     bqkv = None
     if p.get("bq") is not None:
@@ -78,14 +81,31 @@ def prep_vit(p, device):
         for i, k in enumerate(("bq", "bk", "bv")):
             bqkv[i * H:(i + 1) * H].copy_(p[k])
     opt = lambda k: _dev(p[k], device) if p.get(k) is not None else None  # noqa: E731
-    return dict(
+    P = dict(
         wqkv=_pack_cols([p["Wq"], p["Wk"], p["Wv"]], device), bqkv=bqkv,
         wo=ops.pack_weight(_dev(p["Wo"], device)), bo=opt("bo"),
         wup=ops.pack_weight(_dev(p["W_up"], device)), bup=opt("b_up"),
         wd=ops.pack_weight(_dev(p["W_down"], device)), bd=opt("b_down"),
         g1=_dev(p["W_norm_1"], device), b1=opt("b_norm_1"),
         g2=_dev(p["W_norm_2"], device), b2=opt("b_norm_2"),
+        wide=wide,
     )
+    if wide:
+        for k in ("wqkv", "wo", "wup", "wd"):
+            P[k + "_blk"] = ops.slab_block(P[k])
+    return P
+
+
+def vit_wide_ok(cfg: VitConfig, rows: int) -> bool:
+    """True when the 256x256 GEMM takes every ViT projection at ``rows`` rows
+    (the automatic tile choice), so the slab-blocked layouts can be used."""
+    from . import _lib
+    lib = _lib.load()
+    H, I = cfg.hidden, cfg.inter
+    shapes = ((3 * H, H), (H, H), (I, H), (H, I))
+    return rows % 256 == 0 and all(n % 256 == 0 and k % 128 == 0 and
+                                   lib.svla_gemm_tile_choice(rows, n, k, 0) == 8
+                                   for n, k in shapes)
 
 
 @dataclass
@@ -191,6 +211,8 @@ def vit_layer(x, P, cfg: VitConfig, n_img, T, bufs: Optional[Buffers] = None):
     bufs = bufs or Buffers(x.device)
     M = n_img * T
     H = cfg.hidden
+    if P.get("wide"):
+        return _vit_layer_wide(x, P, cfg, n_img, T, bufs)
     h = ops.layernorm(x, P["g1"], P["b1"], cfg.ln_eps, out=bufs.get("vh", M, H))
     qkv = ops.linear(h, P["wqkv"], bias=P["bqkv"], out=bufs.get("vqkv", M, 3 * H))
     q3 = qkv.view(n_img, T, 3 * H)
@@ -202,3 +224,26 @@ def vit_layer(x, P, cfg: VitConfig, n_img, T, bufs: Optional[Buffers] = None):
     act = ops.linear(h, P["wup"], bias=P["bup"], act="gelu_" + cfg.gelu,
                      out=bufs.get("vmlp", M, cfg.inter))
     ops.linear(act, P["wd"], bias=P["bd"], res=x, out=x)
+
+
+def _vit_layer_wide(x, P, cfg: VitConfig, n_img, T, bufs: Buffers):
+    """The same block on the 256x256 GEMM with slab-blocked weights; the MLP
+    hidden activations stay slab-blocked between the up- and the
+    down-projection (the down-projection's K loop then streams both operands
+    as contiguous kilobytes).  Same arithmetic as :func:`vit_layer` on that
+    kernel, bit for bit."""
+    from .ops import LAYOUT_A_BLOCKED as AB, LAYOUT_W_BLOCKED as WB, LAYOUT_C_BLOCKED as CB
+    M, H, I = n_img * T, cfg.hidden, cfg.inter
+    h = ops.layernorm(x, P["g1"], P["b1"], cfg.ln_eps, out=bufs.get("vh", M, H))
+    qkv = ops.linear_wide(h, P["wqkv_blk"], M, 3 * H, H, bias=P["bqkv"],
+                          out=bufs.get("vqkv", M, 3 * H), layout=WB)
+    q3 = qkv.view(n_img, T, 3 * H)
+    attn = bufs.get("vattn", M, H)
+    ops.attention(q3[:, :, :H], q3[:, :, H:2 * H], q3[:, :, 2 * H:], attn.view(n_img, T, H),
+                  cfg.n_heads, cfg.n_heads, "none", 0, scale=1.0 / math.sqrt(cfg.head_dim))
+    ops.linear_wide(attn, P["wo_blk"], M, H, H, bias=P["bo"], res=x, out=x, layout=WB)
+    h = ops.layernorm(x, P["g2"], P["b2"], cfg.ln_eps, out=bufs.get("vh", M, H))
+    act = bufs.get("vmlp", M, I).view(I // 32, M, 32)
+    ops.linear_wide(h, P["wup_blk"], M, I, H, bias=P["bup"], act="gelu_" + cfg.gelu, out=act,
+                    layout=WB | CB)
+    ops.linear_wide(act, P["wd_blk"], M, H, I, bias=P["bd"], res=x, out=x, layout=AB | WB)

@@ -88,6 +88,43 @@ def linear(a, w, bias=None, bias_f32=None, res=None, act=None, alpha=1.0, out=No
     return out
 
 
+LAYOUT_A_BLOCKED, LAYOUT_W_BLOCKED, LAYOUT_C_BLOCKED = 1, 2, 4
+
+
+def slab_block(x, out=None):
+    """Row-major [rows, k] -> slab-blocked [k // 32, rows, 32] (see
+    ``svla_slab_block_bf16``), returned as a flat-shaped [k // 32, rows, 32]
+    tensor."""
+    rows, k = x.shape
+    out = torch.empty(k // 32, rows, 32, dtype=BF16, device=x.device) if out is None else out
+    _lib.call("svla_slab_block_bf16", _ptr(x), _ld(x), _ptr(out), rows, k, _stream())
+    return out
+
+
+def unblock(xb):
+    """Slab-blocked [k // 32, rows, 32] -> row-major [rows, k] (a torch view
+    copy; for checks and hand-over to row-major consumers)."""
+    s, rows, _ = xb.shape
+    return xb.permute(1, 0, 2).reshape(rows, s * 32)
+
+
+def linear_wide(a, w, m, n, k, bias=None, bias_f32=None, res=None, act=None, alpha=1.0,
+                out=None, layout=0):
+    """``svla_linear_wide_bf16``: the 256x256 persistent GEMM with optional
+    slab-blocked A / W / C (``layout`` = OR of the LAYOUT_* flags).  Blocked
+    tensors are [k // 32, rows, 32]; row-major ones are 2-D views."""
+    if out is None:
+        out = (torch.empty(n // 32, m, 32, dtype=BF16, device=a.device) if layout & LAYOUT_C_BLOCKED
+               else torch.empty(m, n, dtype=BF16, device=a.device))
+    lda = 0 if layout & LAYOUT_A_BLOCKED else _ld(a)
+    ldw = 0 if layout & LAYOUT_W_BLOCKED else _ld(w)
+    ldc = 0 if layout & LAYOUT_C_BLOCKED else _ld(out)
+    _lib.call("svla_linear_wide_bf16", _ptr(a), lda, _ptr(w), ldw, _ptr(bias), _ptr(bias_f32),
+              _ptr(res), _ld(res) if res is not None else 0, _ptr(out), ldc, m, n, k,
+              float(alpha), ACT[act], int(layout), _stream())
+    return out
+
+
 def linear_rope(a, w, rope_cols, seq_len, cos_t, sin_t, out=None, norm=None):
     M, K = a.shape
     N = w.shape[0]

@@ -50,7 +50,8 @@ class SmolVLAEngine:
         self.patch_w = pd(P["patch"]["kernel"]).reshape(v.hidden, -1)
         self.patch_b = pd(P["patch"]["bias"])
         self.pos_emb = pd(P["patch"]["pos_emb"])
-        self.vit = [layers.prep_vit(lp, dev) for lp in P["vit"]]
+        wide = layers.vit_wide_ok(v, self.B * cfg.n_cameras * v.tokens)
+        self.vit = [layers.prep_vit(lp, dev, wide=wide) for lp in P["vit"]]
         self.conn_w = ops.pack_weight(pd(P["connector"]["W"]))
         self.embed_table = pd(P["embed"])
         self.state_w = ops.pack_weight(pd(P["state"]["W"]))
