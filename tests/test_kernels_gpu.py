@@ -230,12 +230,14 @@ def test_fused_rmsnorm_prologue(ops, M, K):
     h = ref.rms_norm(x, nw, 1e-5)
     got = ops.linear(x.cuda(), wp, norm=(nw.cuda(), 1e-5))
     assert_close_bf16(got, ref.linear(h, w))
-    # vs the standalone RMSNorm kernel followed by the GEMM: the row statistics
-    # are summed in a different fp32 order, so last-bit flips of the normalised
-    # bf16 operand are allowed: outputs agree to within 2^-6 of their range
+    # vs the standalone RMSNorm kernel followed by the GEMM: the fused path
+    # rounds x * gain to bf16 and applies 1 / rms to the fp32 product, the
+    # standalone kernel rounds x * (1 / rms) * gain, so about half the operand
+    # elements differ in their last bit; after the SiLU-mul epilogue's bf16
+    # roundings of gate and up that is up to ~3 output ulps at the largest
+    # outputs: they agree to within 2^-6 of their range
     def same(a, b):
-        assert_close_bf16(a, b)
-        assert rel_err(a, b) <= 2 ** -6
+        assert_close_bf16(a, b, rel=2 ** -6)
 
     sep = ops.linear(ops.rmsnorm(x.cuda(), nw.cuda(), 1e-5), wp)
     same(got, sep)
@@ -476,6 +478,9 @@ ATTN_CASES = [
     (1, 1024, 1024, 12, 12, "none", 0),
     (2, 17, 17, 3, 1, "prefix_lm", 16),
     (1, 1, 5, 2, 1, "none", 0),
+    (2, 50, 256, 15, 5, "none", 0),     # short queries, full key blocks
+    (1, 64, 320, 15, 5, "none", 0),     # largest 2-wave workgroup
+    (1, 65, 65, 15, 5, "causal", 0),    # smallest 4-wave launch, mostly padding
 ]
 
 

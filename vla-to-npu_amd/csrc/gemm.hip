@@ -1120,16 +1120,20 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
 // (in steps of 32) and each accumulates the whole tile with 16x16x32 MFMAs
 // whose operand fragments come straight from global memory.  Problems this
 // small are latency-bound, so each wave issues the loads of up to KR k-steps
-// at once before any MFMA, and the optional RMS statistics of the A rows are
-// gathered while those loads are in flight.  The 8 partial tiles are summed
-// through LDS and all 512 threads run the epilogue.
+// at once before any MFMA.  The optional RMSNorm of the A rows needs no pass
+// of its own: each wave multiplies its A fragments by the gain only and sums
+// their squares on the way into the MFMAs, so a row's statistics are complete
+// once the partial tiles meet, and the row scale 1 / rms multiplies the summed
+// tile in the epilogue.  The 8 partial tiles (and row sums of squares) are
+// summed through LDS and all 512 threads run the epilogue.
 //
 // Split-K over workgroups (gridDim.z = S > 1, for long-K problems whose grid
 // is far smaller than the chip): workgroup z covers k-steps
-// [z * kps, (z + 1) * kps) and writes its fp32 tile to the workspace; the
-// last of the S workgroups of a tile to arrive (device-scope counter) sums the
-// S partials in split order, runs the epilogue and resets the counter.  No
-// workgroup ever waits for another.
+// [z * kps, (z + 1) * kps) and writes its fp32 tile (and, with the norm, its
+// BM partial row sums of squares) to the workspace; the last of the S
+// workgroups of a tile to arrive (device-scope counter) sums the S partials in
+// split order, runs the epilogue and resets the counter.  No workgroup ever
+// waits for another.
 constexpr int SK_WAVES = 8;
 
 template <int BN, int AMODE, bool NORM, int EPI, int ACT>
@@ -1138,12 +1142,15 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
   constexpr int PS = BN + 4;  // padded LDS row of a partial tile (floats)
   constexpr int NT = SK_WAVES * 64;
   // k-steps whose loads are in flight together (bounded by the 256-VGPR budget
-  // of 8 waves per workgroup)
-  constexpr int KR = NORM ? (BN == 32 ? 4 : 2) : (BN == 32 && AMODE == A_DENSE ? 8 : 4);
+  // of 8 waves per workgroup); 8 waves x 4 steps cover K <= 1024 in one round
+  constexpr int KR = BN == 32 && AMODE == A_DENSE && !NORM ? 8 : 4;
+  // one split's workspace partial: the tile, then (norm) its row sums of squares
+  constexpr int PSZ = BM * BN + (NORM ? BM : 0);
   static_assert((EPI != EPI_ROPE && EPI != EPI_SILU) || BN % 64 == 0, "paired epilogue");
   static_assert(!NORM || AMODE == A_DENSE, "row norm only for dense A");
   __shared__ __attribute__((aligned(16))) float s_part[SK_WAVES][BM * PS];
-  __shared__ float s_rs[NORM ? BM : 1];
+  __shared__ float s_ss[NORM ? SK_WAVES : 1][BM];  // per-wave row sums of squares
+  __shared__ float s_rs[NORM ? BM : 1];            // row scale 1 / rms
   __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1188,14 +1195,19 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
 #pragma unroll
     for (int r = 0; r < KR; ++r) load_step(r, min(base + r, ks1 - 1) * 32 + fk);
   };
-  float rs[TM];
+  float ss[TM];  // norm: this lane's sum of squares of row tm * 16 + fr
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) ss[tm] = 0.f;
   auto mma_step = [&](int r) __attribute__((always_inline)) {
     if constexpr (NORM) {
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          fx[r][tm][j] = f2bf(__fmul_rn(__fmul_rn(bf2f(fx[r][tm][j]), rs[tm]), bf2f(fg[r][j])));
+        for (int j = 0; j < 8; ++j) {
+          const float xv = bf2f(fx[r][tm][j]);
+          ss[tm] = __builtin_fmaf(xv, xv, ss[tm]);
+          fx[r][tm][j] = f2bf(__fmul_rn(xv, bf2f(fg[r][j])));
+        }
     }
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
@@ -1210,44 +1222,8 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
       if (base + r < ks1) mma_step(r);  // wave-uniform; only MFMAs under the branch
   };
 
-  // row statistics (NORM): thread (row = tid / 8, part = tid % 8) sums chunks
-  // part, part + 8, ... of its row; its first 8 chunks are loaded before the
-  // first operand round so both are in flight together
-  constexpr int SB = 8;  // statistics chunks per thread per batch
-  const int srow = tid >> 3, spart = tid & 7;
-  const bf16* xr = p.a + (long)min(m0 + srow, p.M - 1) * p.lda;
-  bf16x8 sv[NORM ? SB : 1];
-  if constexpr (NORM) {
-#pragma unroll
-    for (int i = 0; i < SB; ++i) sv[i] = ld8(xr + min((spart + 8 * i) * 8, p.K - 8));
-  }
-  if (ks0 < ks1) load_round(ks0);
-  if constexpr (NORM) {
-    float ss = 0.f;
-    for (int c0 = 0;; c0 += SB * 64) {
-#pragma unroll
-      for (int i = 0; i < SB; ++i) {
-        const bool in = c0 + (spart + 8 * i) * 8 < p.K;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float f = in ? bf2f(sv[i][e]) : 0.f;
-          ss += f * f;
-        }
-      }
-      if (c0 + SB * 64 >= p.K) break;
-#pragma unroll
-      for (int i = 0; i < SB; ++i)
-        sv[i] = ld8(xr + min(c0 + SB * 64 + (spart + 8 * i) * 8, p.K - 8));
-    }
-    ss += __shfl_xor(ss, 1, 64);
-    ss += __shfl_xor(ss, 2, 64);
-    ss += __shfl_xor(ss, 4, 64);
-    if (spart == 0) s_rs[srow] = 1.0f / sqrtf(ss / (float)p.K + p.norm_eps);
-    __syncthreads();
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) rs[tm] = s_rs[tm * 16 + fr];
-  }
   if (ks0 < ks1) {
+    load_round(ks0);
     mma_round(ks0);
     for (int base = ks0 + KR; base < ks1; base += KR) {
       load_round(base);
@@ -1276,7 +1252,25 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
     for (int tn = 0; tn < TN; ++tn)
       *reinterpret_cast<f32x4*>(&s_part[wave][(tm * 16 + fr) * PS + tn * 16 + 4 * (lane >> 4)]) =
           acc[tn][tm];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      float t = ss[tm];
+      t += __shfl_xor(t, 16, 64);
+      t += __shfl_xor(t, 32, 64);
+      if (lane < 16) s_ss[wave][tm * 16 + lane] = t;
+    }
+  }
   __syncthreads();
+  auto wave_ss = [&](int ml) __attribute__((always_inline)) {
+    float t = s_ss[0][ml];
+#pragma unroll
+    for (int w = 1; w < SK_WAVES; ++w) t += s_ss[w][ml];
+    return t;
+  };
+  auto set_rs = [&](int ml, float sumsq) __attribute__((always_inline)) {
+    s_rs[ml] = 1.0f / sqrtf(sumsq / (float)p.K + p.norm_eps);
+  };
 
   auto wave_sum4 = [&](int ml, int nl) __attribute__((always_inline)) {
     f32x4 t = *reinterpret_cast<const f32x4*>(&s_part[0][ml * PS + nl]);
@@ -1288,7 +1282,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
   constexpr int G4 = BM * BN / 4;  // 4-column groups of the tile
   if (S > 1) {
     const int tile = blockIdx.y * gridDim.x + blockIdx.x;
-    float* wt = p.ws + (long)tile * S * (BM * BN);
+    float* wt = p.ws + (long)tile * S * PSZ;
     // The partials are written and read with device-scope accesses, which
     // go through to the memory side instead of staying in one XCD's L2, and
     // every store is acknowledged (vmcnt = 0) before the barrier that
@@ -1300,10 +1294,15 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
     for (int u = tid; u < G4; u += NT) {
       const int ml = u / (BN / 4), nl = (u - ml * (BN / 4)) * 4;
       const f32x4 v = wave_sum4(ml, nl);
-      float* d = wt + (long)z * (BM * BN) + ml * BN + nl;
+      float* d = wt + (long)z * PSZ + ml * BN + nl;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         __hip_atomic_store(d + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if constexpr (NORM) {
+      if (tid < BM)
+        __hip_atomic_store(wt + (long)z * PSZ + BM * BN + tid, wave_ss(tid), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
@@ -1320,22 +1319,35 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
       const int ml = u / (BN / 4), nl = (u - ml * (BN / 4)) * 4;
       f32x4 t = {0.f, 0.f, 0.f, 0.f};
       for (int zz = 0; zz < S; ++zz) {
-        const float* q = wt + (long)zz * (BM * BN) + ml * BN + nl;
+        const float* q = wt + (long)zz * PSZ + ml * BN + nl;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           t[i] += __hip_atomic_load(q + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
       *reinterpret_cast<f32x4*>(&s_part[0][ml * PS + nl]) = t;
     }
+    if constexpr (NORM) {
+      if (tid < BM) {
+        float t = 0.f;
+        for (int zz = 0; zz < S; ++zz)
+          t += __hip_atomic_load(wt + (long)zz * PSZ + BM * BN + tid, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+        set_rs(tid, t);
+      }
+    }
     if (tid == 0)  // ready for the next call
       __hip_atomic_store(p.ws_cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+  } else if constexpr (NORM) {
+    if (tid < BM) set_rs(tid, wave_ss(tid));
     __syncthreads();
   }
   auto sum4 = [&](int ml, int nl, float v[4]) __attribute__((always_inline)) {
     const f32x4 t = S > 1 ? *reinterpret_cast<const f32x4*>(&s_part[0][ml * PS + nl])
                           : wave_sum4(ml, nl);
+    const float sc = NORM ? p.alpha * s_rs[ml] : p.alpha;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = t[i] * p.alpha;
+    for (int i = 0; i < 4; ++i) v[i] = t[i] * sc;
   };
   // every thread handles ITER output groups: all their loads, then all stores
   constexpr bool PAIRED = EPI == EPI_ROPE || EPI == EPI_SILU;
@@ -1537,7 +1549,8 @@ int pick_split(int tiles, int K, int bm, int bn) {
   }
   S = min(S, max(1, nkf));
   // workspace capacity
-  while (S > 1 && ((size_t)tiles * S * bm * bn > kWsFloats || tiles > kWsTiles)) --S;
+  // (a partial is the fp32 tile plus bm row sums of squares for a fused norm)
+  while (S > 1 && ((size_t)tiles * S * (bm * bn + bm) > kWsFloats || tiles > kWsTiles)) --S;
   return max(S, 1);
 }
 
