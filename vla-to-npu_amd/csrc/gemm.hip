@@ -840,14 +840,21 @@ __device__ __forceinline__ void wide_addend(const GemmArgs& p, int wn0, int g, f
 //  distinct banks pairwise);
 //  phase 2 (row layout): 16 lanes read a 256-byte row (one 16-byte read each:
 //  the swizzle keeps bit 0, so slots 2j, 2j + 1 stay adjacent), add the
-//  row-wise operands (position addend, residual) and store it.
+//  residual (RES) and store it.
 // The staging buffer is private to the wave, whose LDS operations complete
 // in order, so no barrier is needed.
-// NT: streaming (non-temporal) stores.  Outputs without a residual are fresh
-// tensors far larger than the caches (the ViT QKV and MLP activations: 0.45 /
-// 0.6 GB at batch 32), where they measured 6-8% faster; in-place residual
-// updates keep ordinary stores (the residual stream is re-read right away).
-template <int ACT, bool NT>
+// RES (p.res is set): all 8 residual pieces of a chunk (8 rows x 16 bytes
+// per lane) are loaded together, one memory round trip per chunk (the
+// epilogue of the ViT O and down projections is bound by these round trips:
+// 16-19 us per tile with two per chunk).  Holding them any earlier (across
+// phase 1 or the previous chunk) costs registers that the last K round then
+// spills.
+// Without a residual the stores are streaming (non-temporal): those outputs
+// are fresh tensors far larger than the caches (the ViT QKV and MLP
+// activations: 0.45 / 0.6 GB at batch 32), where they measured 6-8% faster;
+// in-place residual updates keep ordinary stores (the residual stream is
+// re-read right away).
+template <int ACT, bool RES>
 __device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WTN][WTM],
                                               const f32x4 (&cb)[WTN], bf16* st, int wm0,
                                               int wn0, int lane) {
@@ -858,6 +865,9 @@ __device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WT
   const float alpha = p.alpha;
   const int j = lane & 15;
   const int ncol = wn0 + 8 * j;
+  // phase-2 piece q (0..7) of chunk c: row c * 32 + 4 q + lane / 16, columns ncol .. ncol + 7
+  // phase-2 batch: pieces (rows) whose loads are in flight together
+  constexpr int NB = RES ? 8 : 4;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
 #pragma unroll
@@ -887,49 +897,42 @@ __device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WT
       }
     }
 #pragma unroll
-    for (int b0 = 0; b0 < 8; b0 += 4) {
-      bf16x8 v[4], ad[4], rs[4];
-      int m[4];
+    for (int b0 = 0; b0 < 8; b0 += NB) {
+      bf16x8 v[NB], rsb[NB];
+      int m[NB];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
+      for (int b = 0; b < NB; ++b) {
         const int r = (b0 + b) * 4 + (lane >> 4);
         m[b] = wm0 + c * 32 + r;
         v[b] = *reinterpret_cast<const bf16x8*>(st_addr(r, 2 * j));
       }
-      if (p.rowadd) {
+      if constexpr (RES) {
 #pragma unroll
-        for (int b = 0; b < 4; ++b)
-          ad[b] = ld8(p.rowadd + (long)(min(m[b], p.M - 1) % p.rowadd_period) * p.N +
-                      min(ncol, p.N - 8));
-      }
-      if (p.res) {
-#pragma unroll
-        for (int b = 0; b < 4; ++b)
-          rs[b] = ld8(p.res + (long)min(m[b], p.M - 1) * p.ldr + min(ncol, p.N - 8));
+        for (int b = 0; b < NB; ++b)
+          rsb[b] = ld8(p.res + (long)min(m[b], p.M - 1) * p.ldr + min(ncol, p.N - 8));
       }
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
+      for (int b = 0; b < NB; ++b) {
         if (m[b] >= p.M || ncol >= p.N) continue;
         bf16x8 o = v[b];
-        if (p.rowadd) {
+        if constexpr (RES) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(ad[b][i]));
-        }
-        if (p.res) {
-#pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rs[b][i]));
+          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rsb[b][i]));
         }
         bf16* dst = p.c_blk ? reinterpret_cast<bf16*>(p.c) + (long)(ncol >> 5) * p.M * WBK +
                                   (long)m[b] * WBK + (ncol & 31)
                             : reinterpret_cast<bf16*>(p.c) + crow(p, m[b]) * p.ldc + ncol;
-        if constexpr (NT) __builtin_nontemporal_store(o, reinterpret_cast<bf16x8*>(dst));
-        else st8(dst, o);
+        if constexpr (RES) st8(dst, o);
+        else __builtin_nontemporal_store(o, reinterpret_cast<bf16x8*>(dst));
       }
     }
   }
 }
 
-template <int AMODE, bool NORM, int EPI, int ACT>
+// RES: the output is p.c + p.res (a separate instantiation: the residual
+// epilogue's registers would otherwise be reserved, and the last K round
+// spill for them, in the kernels that have none)
+template <int AMODE, bool NORM, int EPI, int ACT, bool RES>
 __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   static_assert(AMODE == A_DENSE && !NORM && EPI == EPI_STORE, "wide tile: plain dense GEMM");
   __shared__ __attribute__((aligned(1024))) bf16 sA0[WBM * WBK], sA1[WBM * WBK],
@@ -1101,8 +1104,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
     pin_accumulators(acc);
 
-    if (p.res) wide_epilogue<ACT, false>(p, acc, cb, sOut[wave], wm0, wn0, lane);
-    else wide_epilogue<ACT, true>(p, acc, cb, sOut[wave], wm0, wn0, lane);
+    wide_epilogue<ACT, RES>(p, acc, cb, sOut[wave], wm0, wn0, lane);
     if (!has_next) break;
     L = L_next;
     m0 = mn0;
@@ -1424,8 +1426,12 @@ void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
       hipLaunchKernelGGL((gemm_pipe_kernel<64, 64, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
       break;
     case W256:
-      if constexpr (AMODE == A_DENSE && !NORM && EPI == EPI_STORE)
-        hipLaunchKernelGGL((gemm_wide_kernel<AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      if constexpr (AMODE == A_DENSE && !NORM && EPI == EPI_STORE) {
+        if (p.res)
+          hipLaunchKernelGGL((gemm_wide_kernel<AMODE, NORM, EPI, ACT, true>), grid, dim3(256), 0, s, p);
+        else
+          hipLaunchKernelGGL((gemm_wide_kernel<AMODE, NORM, EPI, ACT, false>), grid, dim3(256), 0, s, p);
+      }
       break;
     default:
       if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
@@ -1585,10 +1591,9 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
   if (AMODE != A_DENSE && act) return SVLA_EINVAL;
   if (p.norm_w && (AMODE != A_DENSE || !svla_aligned16(p.norm_w))) return SVLA_EINVAL;
 
-  const bool plain = AMODE == A_DENSE && !p.norm_w && epi == EPI_STORE;
+  const bool plain = AMODE == A_DENSE && !p.norm_w && epi == EPI_STORE && !p.rowadd;
   const bool wide_rows_ok = !p.out_f32 && p.N % 8 == 0 && p.ldc % 8 == 0 &&
-                            (!p.res || (p.ldr % 8 == 0 && svla_aligned16(p.res))) &&
-                            (!p.rowadd || svla_aligned16(p.rowadd));
+                            (!p.res || (p.ldr % 8 == 0 && svla_aligned16(p.res)));
   const TileCfg t = pick_tile(p.M, p.N, p.K, epi, plain, wide_rows_ok);
   if (p.norm_w && p.K > 2048) return SVLA_EINVAL;  // row statistics keep <= 2048 per row
   const int gm = (p.M + t.bm - 1) / t.bm, gn = (p.N + t.bn - 1) / t.bn;
