@@ -117,7 +117,7 @@ int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void*
  * LDS as contiguous kilobytes (measured on MI355X: ~41 B/clk/CU against
  * ~22 for the 64-byte row pieces of the row-major layout).  lda / ldw / ldc
  * are ignored for blocked matrices.  m % 256 == 0, n % 256 == 0,
- * k % 128 == 0; res (row-major) only with a row-major C.  Same numerics as
+ * k % 128 == 0, k >= 256; res (row-major) only with a row-major C.  Same numerics as
  * svla_linear_bf16.  Replaces the same reference GEMMs (the ViT projections,
  * vla/vision_block_bf16.py:135-169). */
 int svla_linear_wide_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
@@ -131,7 +131,7 @@ int svla_slab_block_bf16(const void* x, int ldx, void* out, int rows, int k, svl
 /* Tuning hook: force the GEMM tile configuration for every later call
  * (0: 256x256/32x32-MFMA, 1: 128x128/32x32, 2: 64x128/16x16, 3: 64x64/16x16,
  * 4: skinny 64x64, 5: skinny 64x32, 6: 128x128/16x16, 7: 128x128 4-stage LDS-DMA
- * pipeline, 8: 256x256 4-stage LDS-DMA pipeline with 128x128 wave tiles, 9: 64x64
+ * pipeline, 8: 256x256 5-stage LDS-DMA pipeline with 128x128 wave tiles, 9: 64x64
  * 4-stage LDS-DMA pipeline), or -1 for the automatic
  * shape-based choice (default).  Process-wide; not thread-safe. */
 int svla_gemm_set_tile(int tile);

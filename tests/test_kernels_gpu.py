@@ -130,7 +130,7 @@ def test_linear_bias_act_residual(ops):
 
 
 @pytest.mark.parametrize("M,N,K", [(300, 264, 128), (1000, 704, 384), (513, 1032, 768),
-                                   (256, 256, 3072), (300, 260, 128)])
+                                   (256, 256, 3072), (300, 260, 128), (520, 512, 256)])
 def test_wide_tile_forced(ops, force_tile, M, N, K):
     """The 256x256 wide kernel (K % 128 == 0, N % 8 == 0) on ragged M / N
     tails, through the plain epilogues it serves: bias + GELU, bias +
@@ -154,6 +154,27 @@ def test_wide_tile_forced(ops, force_tile, M, N, K):
                       (a.float() @ w.float() + bf).to(BF16))
     got = ops.linear(a.cuda(), wp, bias_f32=bf.cuda(), out_f32=True)
     assert rel_err(got, a.float() @ w.float() + bf) < 1e-3
+
+
+@pytest.mark.parametrize("K", [256, 640, 768])
+def test_wide_tile_several_tiles_per_workgroup(ops, force_tile, K):
+    """More tiles than workgroups (25 x 11 = 275 > 256): the K tiles of a
+    workgroup's consecutive tiles stream through one 5-stage LDS ring, so each
+    tile starts at a different ring position (K / 32 = 8, 20, 24 K tiles), and
+    the epilogue stages through the ring.  Checked against the 128x128
+    pipeline kernel (itself checked against the oracle), with bias + GELU and
+    bias + residual."""
+    g = gen(K + 7)
+    M, N = 6400, 2816
+    a, b = randn(g, M, K).cuda(), randn(g, N, std=0.05).cuda()
+    wp = ops.pack_weight(randn(g, K, N, std=0.05).cuda())
+    res = randn(g, M, N).cuda()
+    force_tile(8)
+    got = ops.linear(a, wp, bias=b, act="gelu_tanh")
+    got_res = ops.linear(a, wp, bias=b, res=res)
+    force_tile(7)
+    assert_close_bf16(got, ops.linear(a, wp, bias=b, act="gelu_tanh"))
+    assert_close_bf16(got_res, ops.linear(a, wp, bias=b, res=res))
 
 
 def test_slab_block_roundtrip(ops):

@@ -767,13 +767,14 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
 // of the 4 waves owns a 128 x 128 output tile (8 x 8 MFMA 16x16x32 tiles, 256
 // fp32 accumulators per lane, kept in AGPRs), which halves the LDS bytes read
 // per MFMA FLOP relative to a 64 x 64 wave tile: 16 fragment reads feed 64
-// MFMAs per K step.  Operands stream through a 4-stage ring of LDS buffers
-// (K step 32, 32 KB per stage, 128 KB in total) filled by global_load_lds.
+// MFMAs per K step.  Operands stream through a 5-stage ring of LDS buffers
+// (K step 32, 32 KB per stage, 160 KB in total) filled by global_load_lds.
 // The barrier of step s guarantees stage s + 1 is in LDS, so the fragments of
 // step s + 1 are read into a second register set while the MFMAs of step s
 // run and no LDS latency is exposed; the DMA and fragment reads are spread
-// between the MFMAs.  One barrier per K step, three stages of DMA in flight.
-// Same LDS row swizzle and accumulator layout as gemm_pipe_kernel.
+// between the MFMAs.  One barrier per K step, four stages of DMA in flight;
+// the epilogue stages its output through the ring.  Same LDS row swizzle and
+// accumulator layout as gemm_pipe_kernel.
 //
 // The MFMAs are issued through inline asm with the accumulator tied to an
 // AGPR operand: with the builtin, the register allocator shuffles AGPR-resident
@@ -783,12 +784,24 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
 // MFMA reads the zeroed accumulators and before the epilogue reads results.
 constexpr int WBM = 256, WBN = 256, WBK = 32;
 constexpr int W_DMA = 4;  // 1 KB DMA blocks per wave per operand per stage
+constexpr int W_STAGES = 5;                    // LDS ring depth
+constexpr int W_STAGE = (WBM + WBN) * WBK;     // bf16 elements per stage (32 KB)
 constexpr int WTM = 8, WTN = 8;  // wave tile 128 x 128 = 8 x 8 MFMA tiles
 
 // s_waitcnt immediate (gfx9 encoding): vmcnt split over bits 3:0 and 15:14,
 // expcnt bits 6:4 (7 = no wait), lgkmcnt bits 11:8 (15 = no wait)
 constexpr int waitcnt_imm(int vm, int lgkm) {
   return (vm & 15) | ((vm >> 4) << 14) | (7 << 4) | (lgkm << 8);
+}
+
+// Calls f(std::integral_constant<int, i>{}) for i = 0 .. N - 1 (compile-time
+// indices where a #pragma unroll is not honoured).
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<I + 1, N>(f);
+  }
 }
 
 __device__ __forceinline__ void mfma_agpr(f32x4& acc, const bf16x8& a, const bf16x8& b) {
@@ -807,20 +820,24 @@ __device__ __forceinline__ void pin_accumulators(f32x4 (&acc)[N1][N2]) {
     for (int j = 0; j < N2; ++j) asm volatile("" : "+a"(acc[i][j]));
 }
 
-// Per-column addend of the wide epilogue: bf16 bias + fp32 bias, summed once
-// (fp32), for the 8 MFMA column tiles of a 128-wide wave tile at column wn0.
-__device__ __forceinline__ void wide_addend(const GemmArgs& p, int wn0, int g, f32x4 (&cb)[WTN]) {
+// Per-column addend of the wide epilogue, for the 8 MFMA column tiles of a
+// 128-wide wave tile at column wn0, in two parts: the bf16 bias pieces are
+// loaded early (wide_bias_raw) and only read in the epilogue (wide_addend,
+// which adds the fp32 bias): loads return in order, so consuming a load
+// right away would wait for every DMA issued before it, i.e. drain the ring.
+__device__ __forceinline__ void wide_bias_raw(const GemmArgs& p, int wn0, int g,
+                                              bf16x4 (&braw)[WTN]) {
 #pragma unroll
-  for (int tn = 0; tn < WTN; ++tn) cb[tn] = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (p.bias) {
+  for (int tn = 0; tn < WTN; ++tn)
+    braw[tn] = p.bias ? *reinterpret_cast<const bf16x4*>(p.bias + min(wn0 + tn * 16 + 4 * g, p.N - 4))
+                      : bf16x4{};
+}
+__device__ __forceinline__ void wide_addend(const GemmArgs& p, int wn0, int g,
+                                            const bf16x4 (&braw)[WTN], f32x4 (&cb)[WTN]) {
 #pragma unroll
-    for (int tn = 0; tn < WTN; ++tn) {
-      const bf16x4 b4 =
-          *reinterpret_cast<const bf16x4*>(p.bias + min(wn0 + tn * 16 + 4 * g, p.N - 4));
+  for (int tn = 0; tn < WTN; ++tn)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) cb[tn][i] = bf2f(b4[i]);
-    }
-  }
+    for (int i = 0; i < 4; ++i) cb[tn][i] = bf2f(braw[tn][i]);
   if (p.bias_f32) {
 #pragma unroll
     for (int tn = 0; tn < WTN; ++tn)
@@ -856,9 +873,11 @@ __device__ __forceinline__ void wide_addend(const GemmArgs& p, int wn0, int g, f
 // re-read right away).
 template <int ACT, bool RES>
 __device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WTN][WTM],
-                                              const f32x4 (&cb)[WTN], bf16* st, int wm0,
+                                              const bf16x4 (&braw)[WTN], bf16* st, int wm0,
                                               int wn0, int lane) {
   const int fr = lane & 15, g = lane >> 4;
+  f32x4 cb[WTN];
+  wide_addend(p, wn0, g, braw, cb);
   auto st_addr = [&](int r, int chunk) __attribute__((always_inline)) {
     return st + r * 128 + ((chunk ^ ((r & 7) << 2)) << 2);
   };
@@ -932,20 +951,25 @@ __device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WT
 // RES: the output is p.c + p.res (a separate instantiation: the residual
 // epilogue's registers would otherwise be reserved, and the last K round
 // spill for them, in the kernels that have none)
+//
+// Ring: W_STAGES = 5 stages of one K tile each ([A 256 x 32 | B 256 x 32],
+// 32 KB), 160 KB in all.  K tile j of the workgroup's stream (its tiles' K
+// tiles back to back) lives in stage j % 5; at step j (MFMAs on K tile j,
+// whose fragments are already in registers) stage j % 5 is free and takes K
+// tile j + 5, so four K tiles are in flight while one is read: a DMA has
+// four steps to land (the K loop is bound by DMA latency: with three steps
+// it ran 20-35% below the same loop without DMA, measured on MI355X).  The
+// last step of a tile skips its refill, which leaves that stage free for the
+// epilogue's staging; the first step of the next tile issues the skipped K
+// tile together with its own refill.
 template <int AMODE, bool NORM, int EPI, int ACT, bool RES>
 __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   static_assert(AMODE == A_DENSE && !NORM && EPI == EPI_STORE, "wide tile: plain dense GEMM");
-  __shared__ __attribute__((aligned(1024))) bf16 sA0[WBM * WBK], sA1[WBM * WBK],
-      sA2[WBM * WBK], sA3[WBM * WBK];
-  __shared__ __attribute__((aligned(1024))) bf16 sB0[WBN * WBK], sB1[WBN * WBK],
-      sB2[WBN * WBK], sB3[WBN * WBK];
-  // epilogue staging, 8 KB per wave (32 rows x 128 columns), separate from the
-  // ring so the next tile's DMA can land while this tile is stored
-  __shared__ __attribute__((aligned(1024))) bf16 sOut[4][32 * 128];
+  __shared__ __attribute__((aligned(1024))) bf16 sRing[W_STAGES * W_STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int nk = p.K / WBK;  // K % (4 * WBK) == 0 (checked by the launcher)
+  const int nk = p.K / WBK;  // K % (4 * WBK) == 0 and K >= 8 * WBK (checked by the launcher)
   const int T = p.tiles_m * p.tiles_n, G = gridDim.x;
   // workgroup b takes logical tiles slot(b), slot(b) + G, ...; slot() gives
   // the workgroups of one XCD consecutive logical tiles, and tile_coords turns
@@ -982,16 +1006,15 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
 
   // DMA j of a stage: j < W_DMA -> A block, else B block j - W_DMA; kt is a
   // K tile of the tile whose sources are set
-  auto issue_one = [&](auto SI, int j, int kt) __attribute__((always_inline)) {
-    constexpr int S = decltype(SI)::value;
-    bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
-    bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
+  auto issue_one = [&](int s, int j, int kt) __attribute__((always_inline)) {
+    bf16* st = sRing + s * W_STAGE;
     if (j < W_DMA)
       __builtin_amdgcn_global_load_lds((void*)(a_src[j] + kt * a_ks),
-                                       (lds_ptr_t)(sa + (wave * W_DMA + j) * 512), 16, 0, 0);
+                                       (lds_ptr_t)(st + (wave * W_DMA + j) * 512), 16, 0, 0);
     else
       __builtin_amdgcn_global_load_lds((void*)(b_src[j - W_DMA] + kt * b_ks),
-                                       (lds_ptr_t)(sb + (wave * W_DMA + j - W_DMA) * 512), 16, 0, 0);
+                                       (lds_ptr_t)(st + WBM * WBK + (wave * W_DMA + j - W_DMA) * 512),
+                                       16, 0, 0);
   };
 
   f32x4 acc[WTN][WTM];
@@ -1012,10 +1035,10 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   const int fr = lane & 15, g = lane >> 4;
   const int frag_off = fr * WBK + pswz(fr, g) * 8;  // pswz depends on fr only
   bf16x8 fw[2][WTN], fx[2][WTM];
-  auto read_one = [&](auto SI, auto RI, int f) __attribute__((always_inline)) {
-    constexpr int S = decltype(SI)::value, R = decltype(RI)::value;
-    const bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
-    const bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
+  auto read_one = [&](int s, auto RI, int f) __attribute__((always_inline)) {
+    constexpr int R = decltype(RI)::value;
+    const bf16* sa = sRing + s * W_STAGE;
+    const bf16* sb = sa + WBM * WBK;
     if (f < WTN)
       fw[R][f] = *reinterpret_cast<const bf16x8*>(&sb[(wn * 128 + f * 16) * WBK + frag_off]);
     else
@@ -1025,93 +1048,120 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
 
   // each stage is 2 * W_DMA DMA instructions per wave
   constexpr int kStageVm = 2 * W_DMA;
-  constexpr int kWaitPrologue = waitcnt_imm(3 * kStageVm, 15);  // stage 0 landed
-  constexpr int kWaitStep = waitcnt_imm(2 * kStageVm, 0);       // next stage landed, own reads done
+  constexpr int kWaitPrologue = waitcnt_imm(4 * kStageVm, 15);  // stage 0 landed
+  constexpr int kWaitStep = waitcnt_imm(3 * kStageVm, 0);       // next stage landed, own reads done
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
-  using I2 = std::integral_constant<int, 2>;
-  using I3 = std::integral_constant<int, 3>;
+  auto nxt = [](int s) __attribute__((always_inline)) { return s == W_STAGES - 1 ? 0 : s + 1; };
 
-  // One step of the ring: wait until stage s + 1 is in LDS for every wave and
+  // One step of the ring (stage s holds the K tile whose fragments are in
+  // register set R): wait until stage s + 1 is in LDS for every wave and
   // every wave holds its stage-s fragments, then, between the first 32 of the
-  // 64 MFMAs of stage s: refill stage s's buffer with K tile `next_kt` (one
-  // DMA every 4 MFMAs) and read stage s + 1's fragments into the other
-  // register set (one every 2 MFMAs), so the reads have landed by the next
-  // step.  (In vmcnt terms every VMEM instruction issued after a stage's DMA
-  // counts, stores included; the waits stay conservative.)
-  // (The last step of a tile reads nothing: the next tile's stage-0
-  // fragments are read after the epilogue, so they are not live across it.)
-  auto step = [&](auto SI, auto SN, auto RC, int next_kt, auto READ) __attribute__((always_inline)) {
+  // 64 MFMAs: refill stage s with K tile `kt` (REFILL; one DMA every 4
+  // MFMAs) and read stage s + 1's fragments into the other register set (one
+  // every 2 MFMAs), so the reads have landed by the next step.  EXTRA (the
+  // first step of a tile): extra_kt >= 0 also issues that K tile into stage
+  // `extra_s` right after the barrier.  (In vmcnt terms every VMEM instruction issued
+  // after a stage's DMA counts, stores included; the waits stay
+  // conservative.)  The last step of a tile reads nothing: the next tile's
+  // first fragments are read after the epilogue, so they are not live
+  // across it.
+  auto step = [&](auto RC, int s, int kt, auto READ, auto REFILL, auto EXTRA, int extra_s,
+                  int extra_kt) __attribute__((always_inline)) {
     constexpr int R = decltype(RC)::value;
     using RN = std::integral_constant<int, 1 - R>;
+    const int sn = nxt(s);
     __builtin_amdgcn_s_waitcnt(kWaitStep);
     __builtin_amdgcn_s_barrier();
+    if constexpr (decltype(EXTRA)::value) {
+      if (extra_kt >= 0) {
+#pragma unroll
+        for (int j = 0; j < 2 * W_DMA; ++j) issue_one(extra_s, j, extra_kt);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < WTN * WTM; ++i) {
       mfma_agpr(acc[i / WTM][i % WTM], fw[R][i / WTM], fx[R][i % WTM]);
-      if (i < 32 && i % 4 == 0) issue_one(SI, i / 4, next_kt);
+      if constexpr (decltype(REFILL)::value)
+        if (i < 32 && i % 4 == 0) issue_one(s, i / 4, kt);
       if constexpr (decltype(READ)::value)
-        if (i < 32 && i % 2 == 1) read_one(SN, RN{}, i / 2);
+        if (i < 32 && i % 2 == 1) read_one(sn, RN{}, i / 2);
     }
   };
-  using RD = std::true_type;
-  using NR = std::false_type;
+  using Y = std::true_type;
+  using N = std::false_type;
 
-
-  // prologue of the first tile
+  // prologue of the first tile: K tiles 0 .. 4 into stages 0 .. 4
 #pragma unroll
-  for (int j = 0; j < 2 * W_DMA; ++j) issue_one(I0{}, j, 0);
+  for (int s = 0; s < W_STAGES; ++s) {
 #pragma unroll
-  for (int j = 0; j < 2 * W_DMA; ++j) issue_one(I1{}, j, 1);
-#pragma unroll
-  for (int j = 0; j < 2 * W_DMA; ++j) issue_one(I2{}, j, 2);
-#pragma unroll
-  for (int j = 0; j < 2 * W_DMA; ++j) issue_one(I3{}, j, 3);
+    for (int j = 0; j < 2 * W_DMA; ++j) issue_one(s, j, s);
+  }
   zero_acc();
   __builtin_amdgcn_s_waitcnt(kWaitPrologue);
   __builtin_amdgcn_s_barrier();
 #pragma unroll
-  for (int f = 0; f < WTN + WTM; ++f) read_one(I0{}, I0{}, f);
+  for (int f = 0; f < WTN + WTM; ++f) read_one(0, I0{}, f);
 
+  int s0 = 0;          // stage of the current tile's K tile 0
+  int pend_kt = -1;    // K tile 4 of this tile, deferred by the previous tile's last step
   for (;;) {
     const int wm0 = m0 + wm * 128, wn0 = n0 + wn * 128;
-    for (int kt = 0; kt + 4 < nk; kt += 4) {
-      step(I0{}, I1{}, I0{}, kt + 4, RD{});
-      step(I1{}, I2{}, I1{}, kt + 5, RD{});
-      step(I2{}, I3{}, I0{}, kt + 6, RD{});
-      step(I3{}, I0{}, I1{}, kt + 7, RD{});
+    int s = s0;
+    // steps 0 .. nk - 7 refill with this tile's K tiles 5 .. nk - 2; the
+    // first also issues a deferred K tile 4 into the stage after s0's + 3
+    const int ps = s0 == 0 ? W_STAGES - 1 : s0 - 1;  // (s0 + 4) % 5
+    step(I0{}, s, 5, Y{}, Y{}, Y{}, ps, pend_kt);
+    s = nxt(s);
+    step(I1{}, s, 6, Y{}, Y{}, N{}, 0, 0);
+    s = nxt(s);
+    for (int kt = 2; kt + 6 < nk; kt += 2) {
+      step(I0{}, s, kt + 5, Y{}, Y{}, N{}, 0, 0);
+      s = nxt(s);
+      step(I1{}, s, kt + 6, Y{}, Y{}, N{}, 0, 0);
+      s = nxt(s);
     }
-    // per-column addend of the epilogue (bf16 bias + fp32 bias, summed once),
-    // loaded before the next tile's DMA so that waiting for it does not wait
-    // for that DMA
-    f32x4 cb[WTN];
-    wide_addend(p, wn0, g, cb);
-    // last round: its DMA fetches the next tile's K tiles 0 .. 3 (or, after
-    // the last tile, reloads this tile's last K tile, never read); the wait
-    // of its last step has seen K tile 0 land for every wave
+    // the epilogue's bf16 bias, loaded before the next tile's DMA so that
+    // waiting for it does not wait for that DMA
+    bf16x4 braw[WTN];
+    wide_bias_raw(p, wn0, g, braw);
+    // the last 6 steps: the first refills this tile's K tile nk - 1, the next
+    // four the next tile's K tiles 0 .. 3 (or, after the last tile, reload
+    // this tile's last K tile, never read); the last refills nothing
     const int L_next = L + G;
     const bool has_next = L_next < T;
+    step(I0{}, s, nk - 1, Y{}, Y{}, N{}, 0, 0);
+    s = nxt(s);
     int mn0 = m0, nn0 = n0;
     if (has_next) {
       origin(L_next, mn0, nn0);
       set_src(mn0, nn0);
     }
-    step(I0{}, I1{}, I0{}, has_next ? 0 : nk - 1, RD{});
-    step(I1{}, I2{}, I1{}, has_next ? 1 : nk - 1, RD{});
-    step(I2{}, I3{}, I0{}, has_next ? 2 : nk - 1, RD{});
-    step(I3{}, I0{}, I1{}, has_next ? 3 : nk - 1, NR{});
+    step(I1{}, s, has_next ? 0 : nk - 1, Y{}, Y{}, N{}, 0, 0);
+    s = nxt(s);
+    step(I0{}, s, has_next ? 1 : nk - 1, Y{}, Y{}, N{}, 0, 0);
+    s = nxt(s);
+    step(I1{}, s, has_next ? 2 : nk - 1, Y{}, Y{}, N{}, 0, 0);
+    s = nxt(s);
+    step(I0{}, s, has_next ? 3 : nk - 1, Y{}, Y{}, N{}, 0, 0);
+    s = nxt(s);
+    step(I1{}, s, 0, N{}, N{}, N{}, 0, 0);
     // let the last MFMAs retire before their accumulators are read
     asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
     pin_accumulators(acc);
 
-    wide_epilogue<ACT, RES>(p, acc, cb, sOut[wave], wm0, wn0, lane);
+    // stage s held K tile nk - 1 (its fragments were read at the previous
+    // step, before this step's barrier) and takes no DMA until the next
+    // tile's first step: the epilogue stages through it, 8 KB per wave
+    wide_epilogue<ACT, RES>(p, acc, braw, sRing + s * W_STAGE + wave * (32 * 128), wm0, wn0, lane);
     if (!has_next) break;
     L = L_next;
     m0 = mn0;
     n0 = nn0;
+    s0 = nxt(s);   // the next tile's K tile 0
+    pend_kt = 4;   // goes into stage s, after the next step's barrier
     zero_acc();
-#pragma unroll
-    for (int f = 0; f < WTN + WTM; ++f) read_one(I0{}, I0{}, f);
+    static_for<0, WTN + WTM>([&](auto F) { read_one(s0, I0{}, decltype(F)::value); });
   }
   // drain the trailing (never read) DMA and the stores before exit
   __builtin_amdgcn_s_waitcnt(0);
@@ -1470,8 +1520,9 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok) {
   auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   const bool paired = epi == EPI_ROPE || epi == EPI_SILU;
   const bool pipe_ok = K >= PBK;  // the pipelined kernels need one full K step
-  // whole 4-stage rounds; 16-byte row stores (N, ldc, ldr multiples of 8)
-  const bool wide_ok = plain && K % (4 * WBK) == 0 && wide_rows_ok;
+  // whole 4-step rounds and at least 8 K steps; 16-byte row stores (N, ldc,
+  // ldr multiples of 8)
+  const bool wide_ok = plain && K % (4 * WBK) == 0 && K >= 8 * WBK && wide_rows_ok;
   if (g_force_tile >= 0 && !(paired && g_force_tile == S32)) {
     if (g_force_tile == W256 && !wide_ok) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
     if (g_force_tile == P128 && !pipe_ok) return tile_dims(T128);
@@ -1681,7 +1732,7 @@ int svla_linear_wide_bf16(const void* a, int lda, const void* w, int ldw, const 
                           const float* bias_f32, const void* res, int ldr, void* c, int ldc, int m,
                           int n, int k, float alpha, int act, int layout, svla_stream_t stream) {
   if (act < 0 || act > SVLA_ACT_SILU || (layout & ~7)) return SVLA_EINVAL;
-  if (m <= 0 || m % WBM || n % WBN || k % (4 * WBK)) return SVLA_EINVAL;
+  if (m <= 0 || m % WBM || n % WBN || k % (4 * WBK) || k < 8 * WBK) return SVLA_EINVAL;
   if ((long)m * k > (1L << 31) || (long)n * k > (1L << 31)) return SVLA_EINVAL;
   if (bias_f32 && !svla_aligned16(bias_f32)) return SVLA_EINVAL;
   if (res && ((layout & SVLA_LAYOUT_C_BLOCKED) || ldr % 8 || !svla_aligned16(res))) return SVLA_EINVAL;
