@@ -128,8 +128,8 @@ def dominant_kernel_roofline(eng, iters):
     traffic = tr.get("bytes_per_launch") if tr and tr.get("shape") == [M, v.inter, v.hidden] else None
     from smolvla import _lib
     tile = _lib.load().svla_gemm_tile_choice(M, v.inter, v.hidden, 1)
-    kname = {8: "gemm_wide_kernel<0, false, 0, 1> (persistent 256x256 tile, 4-stage LDS-DMA ring, "
-                "LDS-staged bias + tanh-GELU epilogue" +
+    kname = {8: "gemm_wide_kernel<0, false, 0, 1, false> (persistent 256x256 tile, 5-stage "
+                "LDS-DMA ring, LDS-staged bias + tanh-GELU epilogue, streaming stores" +
                 (", slab-blocked weights and output)" if wide else ")"),
              7: "gemm_pipe_kernel<128, 128, 0, false, 0, 1> (128x128 LDS-DMA pipeline, "
                 "bias + tanh-GELU epilogue)"}.get(tile, f"GEMM tile configuration {tile}")
