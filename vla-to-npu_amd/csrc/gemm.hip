@@ -1446,7 +1446,7 @@ __global__ __launch_bounds__(256) void slab_block_kernel(const bf16* __restrict_
 
 // ---- launch ---------------------------------------------------------------
 enum TileId { T256 = 0, T128 = 1, T64x128 = 2, T64 = 3, S64 = 4, S32 = 5, T128S = 6,
-              P128 = 7, W256 = 8, P64 = 9, NUM_TILES = 10 };
+              P128 = 7, W256 = 8, P64 = 9, P128x64 = 10, P64x128 = 11, NUM_TILES = 12 };
 
 template <int AMODE, bool NORM, int EPI, int ACT>
 void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
@@ -1474,6 +1474,13 @@ void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
       break;
     case P64:
       hipLaunchKernelGGL((gemm_pipe_kernel<64, 64, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      break;
+    case P128x64:
+      if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
+        hipLaunchKernelGGL((gemm_pipe_kernel<128, 64, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      break;
+    case P64x128:
+      hipLaunchKernelGGL((gemm_pipe_kernel<64, 128, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
       break;
     case W256:
       if constexpr (AMODE == A_DENSE && !NORM && EPI == EPI_STORE) {
@@ -1508,6 +1515,8 @@ TileCfg tile_dims(TileId id) {
     case P128: return {P128, 128, 128};
     case W256: return {W256, 256, 256};
     case P64: return {P64, 64, 64};
+    case P128x64: return {P128x64, 128, 64};
+    case P64x128: return {P64x128, 64, 128};
     case T64x128: return {T64x128, 64, 128};
     case T64: return {T64, 64, 64};
     case S64: return {S64, 64, 64};
@@ -1527,6 +1536,8 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok) {
     if (g_force_tile == W256 && !wide_ok) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
     if (g_force_tile == P128 && !pipe_ok) return tile_dims(T128);
     if (g_force_tile == P64 && !pipe_ok) return tile_dims(T64);
+    if ((g_force_tile == P128x64 || g_force_tile == P64x128) && !pipe_ok) return tile_dims(T64);
+    if (g_force_tile == P128x64 && paired) return tile_dims(P64);  // paired needs 64-wide wave tiles
     return tile_dims((TileId)g_force_tile);
   }
   if (M <= kSkinnyMaxM) {
@@ -1545,7 +1556,19 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok) {
   // (gate|up 1600x4096x720: 19 us vs 34 us on 64x64); below that the 64x64
   // LDS-DMA pipeline's larger grid wins
   if (tiles(128, 128) >= kNumCU) return tile_dims(T128);
-  return pipe_ok ? tile_dims(P64) : tile_dims(T64);
+  if (!pipe_ok) return tile_dims(T64);
+  // below that, measured on MI355X: when the 64x64 grid would put one or two
+  // workgroups on each CU (256-512 tiles, uneven), a 128x64 / 64x128 tile
+  // halves the grid to about one per CU (expert at batch 32, M = 1600: O
+  // 12.5 -> 10.9 us, down 19.3 -> 16.9 us, Q + RoPE 12.1 -> 11.0 us; M =
+  // 1928, K = 2560: 25.4 -> 22.4 us); with fewer tiles, or more (the batch-1
+  // ViT's 576), 64x64 stays ahead.  Paired epilogues need 64-wide wave tiles:
+  // 64x128, or 128x128 for large paired grids (QKV + RoPE 1600 x 720:
+  // 17.7 -> 15.2 us).
+  const long t64 = tiles(64, 64);
+  if (t64 >= kNumCU && t64 <= 2 * kNumCU) return tile_dims(paired ? P64x128 : P128x64);
+  if (paired && t64 > 2 * kNumCU && tiles(128, 128) >= kNumCU / 2) return tile_dims(P128);
+  return tile_dims(P64);
 }
 
 // ---- skinny split-K --------------------------------------------------------
