@@ -348,27 +348,13 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
   const int kt_begin = 0;
   const int kt_end = (p.K + BK - 1) / BK;
 
-  // ---- prologue: per-row RMS statistics of this block's A rows
-  if constexpr (NORM) {
-    for (int r = wave; r < BM; r += 4) {
-      const int m = m0 + r;
-      float ss = 0.f;
-      if (m < p.M) {
-        const bf16* xr = p.a + (long)m * p.lda;
-        for (int c = lane * 8; c < p.K; c += 512) {
-          const bf16x8 v = ld8(xr + c);
+  // Fused RMSNorm (NORM): the A chunks are multiplied by the gain on their
+  // way into LDS while their squares are summed (each row's K is spread over
+  // the 8 consecutive threads that own its chunks); the row scale 1 / rms
+  // multiplies the accumulators in the epilogue.  No pass over A of its own.
+  float ssq[NORM ? A_CH : 1];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float f = bf2f(v[j]);
-            ss += f * f;
-          }
-        }
-      }
-      ss = wave_sum(ss);
-      if (lane == 0) s_rs[r] = 1.0f / sqrtf(ss / (float)p.K + p.norm_eps);
-    }
-    __syncthreads();
-  }
+  for (int i = 0; i < (NORM ? A_CH : 1); ++i) ssq[i] = 0.f;
 
   acc_t acc[TN][TM];
 #pragma unroll
@@ -409,11 +395,12 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
       const int c = tid + i * 256;
       bf16x8 v = kin ? ra[i] : bf16x8{};
       if constexpr (NORM) {
-        // torch 2.10 nn.RMSNorm on bf16: fp32 x * rsqrt(.) * w, one rounding
-        const float rs = s_rs[c >> 3];
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          v[j] = f2bf(__fmul_rn(__fmul_rn(bf2f(v[j]), rs), bf2f(rw[j])));
+        for (int j = 0; j < 8; ++j) {
+          const float xv = bf2f(v[j]);
+          ssq[i] = __builtin_fmaf(xv, xv, ssq[i]);
+          v[j] = f2bf(__fmul_rn(xv, bf2f(rw[j])));
+        }
       }
       *reinterpret_cast<bf16x8*>(&sA[buf][(c >> 3) * LDS_STRIDE + (c & 7) * 8]) = v;
     }
@@ -462,6 +449,17 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
       __syncthreads();
     }
   }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) {
+      float t = ssq[i];
+      t += __shfl_xor(t, 1, 64);
+      t += __shfl_xor(t, 2, 64);
+      t += __shfl_xor(t, 4, 64);
+      if ((tid & 7) == 0) s_rs[(tid + i * 256) >> 3] = 1.0f / sqrtf(t / (float)p.K + p.norm_eps);
+    }
+    __syncthreads();
+  }
 
   // ---- accumulator layout: acc[tn][tm][r] = C[m][n] with
   //   m = m0 + wm*WM + tm*MF + lane % MF
@@ -497,10 +495,11 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
         const int n = n0 + wn * WN + tn * MF + q * RUN_STRIDE + col_in;
         if (m >= p.M || n >= p.N) continue;
         float x1[4], x2[4];
+        const float sc = NORM ? p.alpha * s_rs[wm * WM + tm * MF + (lane % MF)] : p.alpha;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          x1[i] = acc[tn][tm][4 * q + i] * p.alpha;
-          x2[i] = PAIRED ? acc[(tn + PAIR_T) % TN][tm][4 * q + i] * p.alpha : 0.f;
+          x1[i] = acc[tn][tm][4 * q + i] * sc;
+          x2[i] = PAIRED ? acc[(tn + PAIR_T) % TN][tm][4 * q + i] * sc : 0.f;
         }
         epi_apply<EPI, ACT>(p, m, n, x1, x2, e[tm * RUNS + q]);
       }
@@ -539,7 +538,6 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
       sA2[BM * PBK], sA3[BM * PBK];
   __shared__ __attribute__((aligned(1024))) bf16 sB0[BN * PBK], sB1[BN * PBK],
       sB2[BN * PBK], sB3[BN * PBK];
-  __shared__ float s_rs[NORM ? BM : 1];
   __shared__ __attribute__((aligned(16))) bf16 s_gain[NORM ? 2048 : 8];  // norm gain (K <= 2048)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -552,23 +550,6 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
   const int nk = p.K / PBK;  // full K steps (>= 1, checked by the launcher)
 
   if constexpr (NORM) {
-    for (int r = wave; r < BM; r += 4) {
-      const int m = m0 + r;
-      float ss = 0.f;
-      if (m < p.M) {
-        const bf16* xr = p.a + (long)m * p.lda;
-        for (int c = lane * 8; c < p.K; c += 512) {
-          const bf16x8 v = ld8(xr + c);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float f = bf2f(v[j]);
-            ss += f * f;
-          }
-        }
-      }
-      ss = wave_sum(ss);
-      if (lane == 0) s_rs[r] = 1.0f / sqrtf(ss / (float)p.K + p.norm_eps);
-    }
     // the gain vector lives in LDS so the main loop issues no global loads
     // besides its DMA (a plain load would force a full vmcnt drain)
     for (int c = tid * 8; c < p.K; c += 256 * 8)
@@ -635,11 +616,14 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
     for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int fr = lane & 15, g = lane >> 4;
-  float rs[TM];
-  if constexpr (NORM) {
+  // Fused RMSNorm (NORM): every wave reads the A fragments of its rows over
+  // the whole K, so it multiplies them by the gain and sums their squares on
+  // the way into the MFMAs (lane: row tm * 16 + fr, columns g * 8 .. + 7 of
+  // each K step); the row scale 1 / rms multiplies the accumulators in the
+  // epilogue.  No pass over A of its own.
+  float ssq[TM];
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) rs[tm] = s_rs[wm * WM + tm * 16 + fr];
-  }
+  for (int tm = 0; tm < TM; ++tm) ssq[tm] = 0.f;
 
   auto normalise = [&](bf16x8 (&fx)[TM], int k) {
     if constexpr (NORM) {
@@ -647,8 +631,11 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
 #pragma unroll
       for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          fx[tm][j] = f2bf(__fmul_rn(__fmul_rn(bf2f(fx[tm][j]), rs[tm]), bf2f(gw[j])));
+        for (int j = 0; j < 8; ++j) {
+          const float xv = bf2f(fx[tm][j]);
+          ssq[tm] = __builtin_fmaf(xv, xv, ssq[tm]);
+          fx[tm][j] = f2bf(__fmul_rn(xv, bf2f(gw[j])));
+        }
     }
   };
   auto mma = [&](const bf16x8 (&fw)[TN], const bf16x8 (&fx)[TM]) {
@@ -728,6 +715,16 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
     normalise(fx, min(k, p.K - 8));  // fx is zero past K whatever the gain
     mma(fw, fx);
   }
+  float rs[TM];  // row scale of row tm * 16 + fr (the lane's epilogue rows)
+  if constexpr (NORM) {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      float t = ssq[tm];
+      t += __shfl_xor(t, 16, 64);
+      t += __shfl_xor(t, 32, 64);
+      rs[tm] = 1.0f / sqrtf(t / (float)p.K + p.norm_eps);
+    }
+  }
 
   // ---- epilogue (same lane layout as gemm_kernel with MF = 16), one column
   // tile at a time: all loads, then all stores
@@ -752,10 +749,11 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
       const int m = m0 + wm * WM + tm * 16 + fr;
       if (m >= p.M || n >= p.N) continue;
       float x1[4], x2[4];
+      const float sc = NORM ? p.alpha * rs[tm] : p.alpha;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        x1[i] = acc[tn][tm][i] * p.alpha;
-        x2[i] = PAIRED ? acc[(tn + 2) % TN][tm][i] * p.alpha : 0.f;
+        x1[i] = acc[tn][tm][i] * sc;
+        x2[i] = PAIRED ? acc[(tn + 2) % TN][tm][i] * sc : 0.f;
       }
       epi_apply<EPI, ACT>(p, m, n, x1, x2, e[tm]);
     }
