@@ -95,7 +95,8 @@ int svla_layernorm_bf16(const void* x, int ldx, const void* gamma, const void* b
  * norm_w (may be NULL): the A rows are RMS-normalised on the fly,
  *   C[m,n] = rsqrt(mean_k(x[m,:]^2) + norm_eps) * sum_k bf16(x[m,k] * norm_w[k]) * W[n,k]
  * (the scale applied to the fp32 product, before the epilogue: the same
- * normalised product as bf16(x * rsqrt(.) * w) . W up to one bf16 rounding)
+ * normalised product as bf16(x * rsqrt(.) * w) . W up to one bf16 rounding);
+ * K <= 2048.
  * (the rmsnorm() that precedes every projection, vla/text_encoder_bf16.py:398-404).
  * Epilogue order (mirrors the torch modules' bf16 boundaries):
  *   v = alpha*acc (+ bias[n]) (+ bias_f32[n]); if out_f32: store fp32 v.
