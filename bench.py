@@ -82,16 +82,17 @@ def time_chunks(eng, n):
 
 def _up_proj_launcher(cfg, M, x, w_packed, bias, wide):
     """The ViT MLP up-projection exactly as the engine launches it at this
-    row count: on the 256x256 kernel with slab-blocked weights and a
-    slab-blocked output when ``wide`` (``layers.vit_wide_ok``), else through
-    ``ops.linear``."""
+    row count: on the 256x256 kernel with slab-blocked activations (the
+    LayerNorm writes them so), weights and output when ``wide``
+    (``layers.vit_wide_ok``), else through ``ops.linear``."""
     from smolvla import ops
     v = cfg.vit
     if wide:
+        xb = ops.slab_block(x)
         wb = ops.slab_block(w_packed)
         out = torch.empty(v.inter // 32, M, 32, device="cuda", dtype=torch.bfloat16)
-        lay = ops.LAYOUT_W_BLOCKED | ops.LAYOUT_C_BLOCKED
-        return lambda: ops.linear_wide(x, wb, M, v.inter, v.hidden, bias=bias,
+        lay = ops.LAYOUT_A_BLOCKED | ops.LAYOUT_W_BLOCKED | ops.LAYOUT_C_BLOCKED
+        return lambda: ops.linear_wide(xb, wb, M, v.inter, v.hidden, bias=bias,
                                        act="gelu_" + v.gelu, out=out, layout=lay)
     out = torch.empty(M, v.inter, device="cuda", dtype=torch.bfloat16)
     return lambda: ops.linear(x, w_packed, bias=bias, act="gelu_" + v.gelu, out=out)
@@ -130,7 +131,7 @@ def dominant_kernel_roofline(eng, iters):
     tile = _lib.load().svla_gemm_tile_choice(M, v.inter, v.hidden, 1)
     kname = {8: "gemm_wide_kernel<0, false, 0, 1, false> (persistent 256x256 tile, 5-stage "
                 "LDS-DMA ring, LDS-staged bias + tanh-GELU epilogue, streaming stores" +
-                (", slab-blocked weights and output)" if wide else ")"),
+                (", slab-blocked activations, weights and output)" if wide else ")"),
              7: "gemm_pipe_kernel<128, 128, 0, false, 0, 1> (128x128 LDS-DMA pipeline, "
                 "bias + tanh-GELU epilogue)"}.get(tile, f"GEMM tile configuration {tile}")
     return {

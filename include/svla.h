@@ -85,6 +85,13 @@ int svla_rmsnorm_bf16(const void* x, int ldx, const void* w, void* y, int ldy, i
 int svla_layernorm_bf16(const void* x, int ldx, const void* gamma, const void* beta, void* y,
                         int ldy, int rows, int cols, float eps, svla_stream_t stream);
 
+/* svla_layernorm_bf16 writing its output slab-blocked, [cols/32][rows][32] (the
+ * A layout of svla_linear_wide_bf16 with SVLA_LAYOUT_A_BLOCKED); cols % 32 == 0.
+ * Same values.  Replaces the same reference LayerNorm (vla/vision_block_bf16.py:101-127)
+ * where its output feeds the big-batch ViT projections. */
+int svla_layernorm_blocked_bf16(const void* x, int ldx, const void* gamma, const void* beta,
+                                void* y, int rows, int cols, float eps, svla_stream_t stream);
+
 /* ----------------------------------------------------------------- GEMM --
  * C[M,N] = epilogue(alpha * norm(A)[M,K] . W[N,K]^T) on bf16 MFMA (fp32 accumulate).
  * Replaces the Allo GEMM module GEMM(M,N,K,Pm,Pn,Pk,bf16,bf16) and its K-chunk

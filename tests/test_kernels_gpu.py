@@ -84,6 +84,17 @@ def test_layernorm(ops, rows, cols):
     got = ops.layernorm(x.cuda(), gm.cuda(), bt.cuda(), 1e-6)
     want = ref.layer_norm(x, gm, bt, 1e-6)
     torch.testing.assert_close(got.cpu().float(), want.float(), atol=1e-2, rtol=2 ** -7)
+    # the slab-blocked output holds the same values, bit for bit
+    blk = ops.layernorm(x.cuda(), gm.cuda(), bt.cuda(), 1e-6, blocked=True)
+    assert blk.shape == (cols // 32, rows, 32)
+    assert torch.equal(ops.unblock(blk), got)
+
+
+def test_layernorm_blocked_rejects_bad_cols(ops):
+    from smolvla._lib import SvlaError
+    x = torch.zeros(4, 80, dtype=BF16, device="cuda")
+    with pytest.raises(SvlaError):
+        ops.layernorm(x, x[0], x[0], 1e-6, blocked=True)    # cols % 32 != 0
 
 
 # ------------------------------------------------------------------- GEMM ---

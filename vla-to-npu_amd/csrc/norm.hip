@@ -51,6 +51,10 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16* __restrict__ x
   }
 }
 
+// BLK: y is slab-blocked, element (row, c) at (c / 32) * rows * 32 + row * 32 +
+// c % 32 (the A layout the 256x256 GEMM streams as contiguous kilobytes); each
+// lane's 16-byte chunk stays inside one 64-byte slab row.
+template <bool BLK>
 __global__ __launch_bounds__(256) void layernorm_kernel(const bf16* __restrict__ x, long ldx,
                                                         const bf16* __restrict__ gmm,
                                                         const bf16* __restrict__ bta,
@@ -96,7 +100,10 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const bf16* __restrict__
 #pragma unroll
       for (int j = 0; j < 8; ++j)
         o[j] = f2bf((bf2f(v[i][j]) - mean) * rstd * bf2f(gv[j]) + bf2f(bv[j]));
-      st8(yr + c, o);
+      if constexpr (BLK)
+        st8(y + (long)(c >> 5) * rows * 32 + (long)row * 32 + (c & 31), o);
+      else
+        st8(yr + c, o);
     }
   }
 }
@@ -126,10 +133,25 @@ extern "C" int svla_layernorm_bf16(const void* x, int ldx, const void* gamma, co
     return SVLA_EINVAL;
   if (beta && !svla_aligned16(beta)) return SVLA_EINVAL;
   if (rows == 0) return SVLA_OK;
-  hipLaunchKernelGGL(layernorm_kernel, dim3((rows + 3) / 4), dim3(256), 0, (hipStream_t)stream,
-                     static_cast<const bf16*>(x), (long)ldx, static_cast<const bf16*>(gamma),
-                     static_cast<const bf16*>(beta), static_cast<bf16*>(y), (long)ldy, rows, cols,
-                     eps);
+  hipLaunchKernelGGL(layernorm_kernel<false>, dim3((rows + 3) / 4), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<const bf16*>(x), (long)ldx,
+                     static_cast<const bf16*>(gamma), static_cast<const bf16*>(beta),
+                     static_cast<bf16*>(y), (long)ldy, rows, cols, eps);
+  SVLA_CHECK_LAUNCH();
+  return SVLA_OK;
+}
+
+extern "C" int svla_layernorm_blocked_bf16(const void* x, int ldx, const void* gamma,
+                                           const void* beta, void* y, int rows, int cols,
+                                           float eps, svla_stream_t stream) {
+  if (cols % 32 || !norm_args_ok(x, ldx, y, cols, cols) || !svla_aligned16(gamma) || rows < 0)
+    return SVLA_EINVAL;
+  if (beta && !svla_aligned16(beta)) return SVLA_EINVAL;
+  if (rows == 0) return SVLA_OK;
+  hipLaunchKernelGGL(layernorm_kernel<true>, dim3((rows + 3) / 4), dim3(256), 0,
+                     (hipStream_t)stream, static_cast<const bf16*>(x), (long)ldx,
+                     static_cast<const bf16*>(gamma), static_cast<const bf16*>(beta),
+                     static_cast<bf16*>(y), 0L, rows, cols, eps);
   SVLA_CHECK_LAUNCH();
   return SVLA_OK;
 }

@@ -23,6 +23,7 @@ SIGNATURES = {
     "svla_version": [],
     "svla_rmsnorm_bf16": [_p, _i, _p, _p, _i, _i, _i, _f, _p],
     "svla_layernorm_bf16": [_p, _i, _p, _p, _p, _i, _i, _i, _f, _p],
+    "svla_layernorm_blocked_bf16": [_p, _i, _p, _p, _p, _i, _i, _f, _p],
     "svla_gemm_set_tile": [_i],
     "svla_gemm_set_split": [_i],
     "svla_gemm_tile_choice": [_i, _i, _i, _i],

@@ -230,23 +230,24 @@ def vit_layer(x, P, cfg: VitConfig, n_img, T, bufs: Optional[Buffers] = None):
 
 
 def _vit_layer_wide(x, P, cfg: VitConfig, n_img, T, bufs: Buffers):
-    """The same block on the 256x256 GEMM with slab-blocked weights; the MLP
-    hidden activations stay slab-blocked between the up- and the
-    down-projection (the down-projection's K loop then streams both operands
-    as contiguous kilobytes).  Same arithmetic as :func:`vit_layer` on that
-    kernel, bit for bit."""
+    """The same block on the 256x256 GEMM with slab-blocked weights; the
+    LayerNorm outputs and the MLP hidden activations are written slab-blocked
+    too, so every projection's K loop streams both operands as contiguous
+    kilobytes (the residual stream stays row-major).  Same arithmetic as
+    :func:`vit_layer` on that kernel, bit for bit."""
     from .ops import LAYOUT_A_BLOCKED as AB, LAYOUT_W_BLOCKED as WB, LAYOUT_C_BLOCKED as CB
     M, H, I = n_img * T, cfg.hidden, cfg.inter
-    h = ops.layernorm(x, P["g1"], P["b1"], cfg.ln_eps, out=bufs.get("vh", M, H))
-    qkv = ops.linear_wide(h, P["wqkv_blk"], M, 3 * H, H, bias=P["bqkv"],
-                          out=bufs.get("vqkv", M, 3 * H), layout=WB)
+    hb = bufs.get("vh", M, H).view(H // 32, M, 32)
+    ops.layernorm(x, P["g1"], P["b1"], cfg.ln_eps, out=hb, blocked=True)
+    qkv = ops.linear_wide(hb, P["wqkv_blk"], M, 3 * H, H, bias=P["bqkv"],
+                          out=bufs.get("vqkv", M, 3 * H), layout=AB | WB)
     q3 = qkv.view(n_img, T, 3 * H)
     attn = bufs.get("vattn", M, H)
     ops.attention(q3[:, :, :H], q3[:, :, H:2 * H], q3[:, :, 2 * H:], attn.view(n_img, T, H),
                   cfg.n_heads, cfg.n_heads, "none", 0, scale=1.0 / math.sqrt(cfg.head_dim))
     ops.linear_wide(attn, P["wo_blk"], M, H, H, bias=P["bo"], res=x, out=x, layout=WB)
-    h = ops.layernorm(x, P["g2"], P["b2"], cfg.ln_eps, out=bufs.get("vh", M, H))
+    ops.layernorm(x, P["g2"], P["b2"], cfg.ln_eps, out=hb, blocked=True)
     act = bufs.get("vmlp", M, I).view(I // 32, M, 32)
-    ops.linear_wide(h, P["wup_blk"], M, I, H, bias=P["bup"], act="gelu_" + cfg.gelu, out=act,
-                    layout=WB | CB)
+    ops.linear_wide(hb, P["wup_blk"], M, I, H, bias=P["bup"], act="gelu_" + cfg.gelu, out=act,
+                    layout=AB | WB | CB)
     ops.linear_wide(act, P["wd_blk"], M, H, I, bias=P["bd"], res=x, out=x, layout=AB | WB)

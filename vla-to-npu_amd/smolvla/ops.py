@@ -62,8 +62,15 @@ def rmsnorm(x, w, eps, out=None):
     return out
 
 
-def layernorm(x, g, b, eps, out=None):
+def layernorm(x, g, b, eps, out=None, blocked=False):
+    """LayerNorm of the rows of ``x``; ``blocked`` writes the slab-blocked
+    ``[cols/32, rows, 32]`` layout (``LAYOUT_A_BLOCKED`` of :func:`linear_wide`)."""
     rows, cols = x.shape
+    if blocked:
+        out = torch.empty(cols // 32, rows, 32, dtype=BF16, device=x.device) if out is None else out
+        _lib.call("svla_layernorm_blocked_bf16", _ptr(x), _ld(x), _ptr(g), _ptr(b), _ptr(out),
+                  rows, cols, float(eps), _stream())
+        return out
     out = torch.empty(rows, cols, dtype=BF16, device=x.device) if out is None else out
     _lib.call("svla_layernorm_bf16", _ptr(x), _ld(x), _ptr(g), _ptr(b), _ptr(out), _ld(out),
               rows, cols, float(eps), _stream())
