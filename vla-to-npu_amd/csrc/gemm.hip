@@ -885,6 +885,20 @@ __device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WT
   // phase-2 piece q (0..7) of chunk c: row c * 32 + 4 q + lane / 16, columns ncol .. ncol + 7
   // phase-2 batch: pieces (rows) whose loads are in flight together
   constexpr int NB = RES ? 8 : 4;
+  // A wave tile inside the matrix (every tile when M and N are multiples of
+  // 256) stores without checks through running pointers: the lane's rows are
+  // wm0 + lane / 16 + 4 i for i = 0 .. 31 in store order, so each store is
+  // one pointer increment (per-store row arithmetic and bounds checks were
+  // most of the epilogue's instructions).  Ragged tiles take a rolled,
+  // checked loop.
+  const bool full = wm0 + 128 <= p.M && wn0 + 128 <= p.N;
+  bf16* const cbase = reinterpret_cast<bf16*>(p.c);
+  const int r0 = wm0 + (lane >> 4);
+  bf16* cp = p.c_blk ? cbase + (long)(ncol >> 5) * p.M * WBK + (long)r0 * WBK + (ncol & 31)
+                     : cbase + (long)r0 * p.ldc + ncol;
+  const long cstep = 4 * (p.c_blk ? (long)WBK : (long)p.ldc);
+  const bf16* rp = RES && full ? p.res + (long)r0 * p.ldr + ncol : nullptr;
+  const long rstep = 4 * (long)p.ldr;
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
 #pragma unroll
@@ -913,34 +927,48 @@ __device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WT
         asm volatile("" : "+a"(acc[tn][2 * c + 3]));
       }
     }
+    if (full) {
 #pragma unroll
-    for (int b0 = 0; b0 < 8; b0 += NB) {
-      bf16x8 v[NB], rsb[NB];
-      int m[NB];
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        const int r = (b0 + b) * 4 + (lane >> 4);
-        m[b] = wm0 + c * 32 + r;
-        v[b] = *reinterpret_cast<const bf16x8*>(st_addr(r, 2 * j));
-      }
-      if constexpr (RES) {
+      for (int b0 = 0; b0 < 8; b0 += NB) {
+        bf16x8 v[NB], rsb[NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b)
-          rsb[b] = ld8(p.res + (long)min(m[b], p.M - 1) * p.ldr + min(ncol, p.N - 8));
-      }
-#pragma unroll
-      for (int b = 0; b < NB; ++b) {
-        if (m[b] >= p.M || ncol >= p.N) continue;
-        bf16x8 o = v[b];
+          v[b] = *reinterpret_cast<const bf16x8*>(st_addr((b0 + b) * 4 + (lane >> 4), 2 * j));
         if constexpr (RES) {
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rsb[b][i]));
+          for (int b = 0; b < NB; ++b) {
+            rsb[b] = ld8(rp);
+            rp += rstep;
+          }
         }
-        bf16* dst = p.c_blk ? reinterpret_cast<bf16*>(p.c) + (long)(ncol >> 5) * p.M * WBK +
-                                  (long)m[b] * WBK + (ncol & 31)
-                            : reinterpret_cast<bf16*>(p.c) + crow(p, m[b]) * p.ldc + ncol;
-        if constexpr (RES) st8(dst, o);
-        else __builtin_nontemporal_store(o, reinterpret_cast<bf16x8*>(dst));
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          bf16x8 o = v[b];
+          if constexpr (RES) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rsb[b][i]));
+            st8(cp, o);
+          } else {
+            __builtin_nontemporal_store(o, reinterpret_cast<bf16x8*>(cp));
+          }
+          cp += cstep;
+        }
+      }
+    } else {
+#pragma unroll 1
+      for (int q = 0; q < 8; ++q) {
+        const int r = q * 4 + (lane >> 4);
+        const int m = wm0 + c * 32 + r;
+        if (m >= p.M || ncol >= p.N) continue;  // ncol < N: all 8 columns (N % 8 == 0)
+        bf16x8 o = *reinterpret_cast<const bf16x8*>(st_addr(r, 2 * j));
+        if constexpr (RES) {
+          const bf16x8 rv = ld8(p.res + (long)m * p.ldr + ncol);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[i] = f2bf(bf2f(o[i]) + bf2f(rv[i]));
+        }
+        st8(p.c_blk ? cbase + (long)(ncol >> 5) * p.M * WBK + (long)m * WBK + (ncol & 31)
+                    : cbase + (long)m * p.ldc + ncol,
+            o);
       }
     }
   }
@@ -1663,7 +1691,8 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
   if (AMODE != A_DENSE && act) return SVLA_EINVAL;
   if (p.norm_w && (AMODE != A_DENSE || !svla_aligned16(p.norm_w))) return SVLA_EINVAL;
 
-  const bool plain = AMODE == A_DENSE && !p.norm_w && epi == EPI_STORE && !p.rowadd;
+  const bool plain =
+      AMODE == A_DENSE && !p.norm_w && epi == EPI_STORE && !p.rowadd && p.c_rpg <= 0;
   const bool wide_rows_ok = !p.out_f32 && p.N % 8 == 0 && p.ldc % 8 == 0 &&
                             (!p.res || (p.ldr % 8 == 0 && svla_aligned16(p.res)));
   const TileCfg t = pick_tile(p.M, p.N, p.K, epi, plain, wide_rows_ok);
