@@ -142,8 +142,8 @@ int svla_slab_block_bf16(const void* x, int ldx, void* out, int rows, int k, svl
  * (0: 256x256/32x32-MFMA, 1: 128x128/32x32, 2: 64x128/16x16, 3: 64x64/16x16,
  * 4: skinny 64x64, 5: skinny 64x32, 6: 128x128/16x16, 7: 128x128 4-stage LDS-DMA
  * pipeline, 8: 256x256 5-stage LDS-DMA pipeline with 128x128 wave tiles, 9: 64x64
- * 4-stage LDS-DMA pipeline, 10: 128x64 and 11: 64x128 4-stage LDS-DMA pipelines), or -1 for
- * the automatic
+ * 4-stage LDS-DMA pipeline, 10: 128x64 and 11: 64x128 4-stage LDS-DMA pipelines, 12: skinny
+ * 64x16), or -1 for the automatic
  * shape-based choice (default).  Process-wide; not thread-safe. */
 int svla_gemm_set_tile(int tile);
 

@@ -287,7 +287,7 @@ def test_fused_rmsnorm_prologue(ops, M, K):
 
 TILES = {0: "256x256/32", 1: "128x128/32", 2: "64x128/16", 3: "64x64/16", 4: "skinny64",
          5: "skinny32", 6: "128x128/16", 7: "pipe128", 8: "wide256", 9: "pipe64",
-         10: "pipe128x64", 11: "pipe64x128"}
+         10: "pipe128x64", 11: "pipe64x128", 12: "skinny16"}
 
 
 @pytest.fixture
@@ -314,7 +314,7 @@ def test_every_tile_config_every_epilogue(ops, force_tile, tile):
     _every_epilogue(ops, gen(100 + tile), tile)
 
 
-@pytest.mark.parametrize("tile,splits", [(4, 2), (5, 3), (4, 6), (5, 8)])
+@pytest.mark.parametrize("tile,splits", [(4, 2), (5, 3), (4, 6), (5, 8), (12, 2), (12, 5)])
 def test_skinny_split_k_every_epilogue(ops, force_tile, force_split, tile, splits):
     """Skinny kernels with K split over `splits` workgroups (partials summed
     by the last one to arrive), through every epilogue and gather; the K tail
@@ -353,6 +353,27 @@ def test_skinny_split_k_graph_replays(ops, force_split):
         ops.linear(a[:17], wp, out=torch.empty(17, 720, dtype=BF16, device="cuda"))
     small = ops.linear(a[:9, :1536], ops.pack_weight(w[:1536].cuda()))
     assert_close_bf16(small, ref.linear(a[:9, :1536].cpu(), w[:1536]))
+
+
+@pytest.mark.parametrize("M,K", [(50, 720), (241, 960)])
+def test_skinny16_paired_matches_skinny64(ops, force_tile, M, K):
+    """The 16-column skinny tile pairs packed columns n and n + 32 through a
+    row map of the weight loads; with the fused RMSNorm both tiles split K
+    over the waves identically, so RoPE and SiLU outputs are bit-identical to
+    the 64-column tile's."""
+    g = gen(41)
+    x = randn(g, M, K).cuda()
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16).cuda()
+    wqkv = ops.pack_weight(randn(g, K, 1600, std=0.02).cuda())
+    wgu = ops.pack_gate_up(randn(g, K, 2048, std=0.02).cuda(), randn(g, K, 2048, std=0.02).cuda())
+    c, s_ = ops.rope_table(M, 64, 1e5)
+    outs = {}
+    for tile in (4, 12):
+        force_tile(tile)
+        outs[tile] = (ops.linear_rope(x, wqkv, 1280, M, c, s_, norm=(nw, 1e-5)),
+                      ops.linear_silu_mul(x, wgu, norm=(nw, 1e-5)))
+    assert torch.equal(outs[4][0], outs[12][0])
+    assert torch.equal(outs[4][1], outs[12][1])
 
 
 def _every_epilogue(ops, g, tile):

@@ -1221,10 +1221,18 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
   constexpr int NT = SK_WAVES * 64;
   // k-steps whose loads are in flight together (bounded by the 256-VGPR budget
   // of 8 waves per workgroup); 8 waves x 4 steps cover K <= 1024 in one round
-  constexpr int KR = BN == 32 && AMODE == A_DENSE && !NORM ? 8 : 4;
+  constexpr int KR = BN <= 32 && AMODE == A_DENSE && !NORM ? 8 : 4;
   // one split's workspace partial: the tile, then (norm) its row sums of squares
   constexpr int PSZ = BM * BN + (NORM ? BM : 0);
-  static_assert((EPI != EPI_ROPE && EPI != EPI_SILU) || BN % 64 == 0, "paired epilogue");
+  // Paired epilogues (RoPE / SiLU) combine packed column n with n + 32 of the
+  // same 64-column block.  A 64-wide tile holds both halves; a 16-wide tile
+  // (P16) takes 8 columns of a first half and their 8 partners, loading the
+  // weight rows through that map (each lane reads its own row anyway): tile t
+  // covers columns pbase + 0..7 and pbase + 32 + 0..7, pbase = 64 (t / 4) +
+  // 8 (t % 4), held at tile columns 0..7 and 8..15.
+  constexpr bool PAIRED = EPI == EPI_ROPE || EPI == EPI_SILU;
+  constexpr bool P16 = PAIRED && BN == 16;
+  static_assert(!PAIRED || BN % 64 == 0 || P16, "paired epilogue");
   static_assert(!NORM || AMODE == A_DENSE, "row norm only for dense A");
   __shared__ __attribute__((aligned(16))) float s_part[SK_WAVES][BM * PS];
   __shared__ float s_ss[NORM ? SK_WAVES : 1][BM];  // per-wave row sums of squares
@@ -1233,6 +1241,8 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  // first packed column of the tile's logical columns (P16: see above)
+  const int nbase = P16 ? (n0 >> 6) * 64 + ((n0 & 63) >> 4) * 8 : n0;
   const int nkf = p.K / 32;  // full k-steps; a K % 32 tail is one extra step
   const int S = gridDim.z, z = blockIdx.z;
   const int kps = (nkf + S - 1) / S;  // k-steps of one split
@@ -1259,7 +1269,8 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) a_rows[tm] = min(m0 + tm * 16 + fr, p.M - 1);
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn) b_rows[tn] = min(n0 + tn * 16 + fr, p.N - 1);
+  for (int tn = 0; tn < TN; ++tn)
+    b_rows[tn] = P16 ? nbase + (fr & 7) + (fr >> 3) * 32 : min(n0 + tn * 16 + fr, p.N - 1);
 
   bf16x8 fw[KR][TN], fx[KR][TM], fg[KR];
   auto load_step = [&](int r, int k) __attribute__((always_inline)) {
@@ -1428,30 +1439,33 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
     for (int i = 0; i < 4; ++i) v[i] = t[i] * sc;
   };
   // every thread handles ITER output groups: all their loads, then all stores
-  constexpr bool PAIRED = EPI == EPI_ROPE || EPI == EPI_SILU;
-  // units per row: 4-column groups (paired: of the first half of each 64-block)
-  constexpr int UPR = PAIRED ? BN / 64 * 8 : BN / 4;
-  constexpr int ITER = BM * UPR / NT;
-  static_assert(ITER * NT == BM * UPR, "epilogue units");
+  // units per row: 4-column groups (paired: of the first half of each 64-block,
+  // or of tile columns 0..7 for P16); the partner sits POFF tile columns on
+  constexpr int UPR = P16 ? 2 : PAIRED ? BN / 64 * 8 : BN / 4;
+  constexpr int POFF = P16 ? 8 : 32;
+  // (a 16-column tile has 256 units: threads past them load in-tile unit 0
+  // and store nothing)
+  constexpr int UNITS = BM * UPR, ITER = (UNITS + NT - 1) / NT;
+  static_assert(UNITS % NT == 0 || UNITS < NT, "epilogue units");
   int ml[ITER], nl[ITER], gm[ITER], gn[ITER];
   EpiIn e[ITER];
 #pragma unroll
   for (int it = 0; it < ITER; ++it) {
-    const int u = tid + it * NT;
+    const int u = UNITS < NT && tid >= UNITS ? 0 : tid + it * NT;
     ml[it] = u / UPR;
     const int r = u - ml[it] * UPR;
-    nl[it] = PAIRED ? (r >> 3) * 64 + (r & 7) * 4 : r * 4;
+    nl[it] = PAIRED && !P16 ? (r >> 3) * 64 + (r & 7) * 4 : r * 4;
     gm[it] = min(m0 + ml[it], p.M - 1);
-    gn[it] = min(n0 + nl[it], p.N - 4);
+    gn[it] = min(nbase + nl[it], p.N - 4);
   }
   epi_load_groups<EPI, ITER>(p, gm, gn, e);
 #pragma unroll
   for (int it = 0; it < ITER; ++it) {
-    const int m = m0 + ml[it], n = n0 + nl[it];
-    if (m >= p.M || n >= p.N) continue;
+    const int m = m0 + ml[it], n = nbase + nl[it];
+    if (m >= p.M || n >= p.N || (UNITS < NT && tid >= UNITS)) continue;
     float x1[4], x2[4];
     sum4(ml[it], nl[it], x1);
-    if constexpr (PAIRED) sum4(ml[it], nl[it] + 32, x2);
+    if constexpr (PAIRED) sum4(ml[it], nl[it] + POFF, x2);
     epi_apply<EPI, ACT>(p, m, n, x1, x2, e[it]);
   }
 }
@@ -1472,7 +1486,7 @@ __global__ __launch_bounds__(256) void slab_block_kernel(const bf16* __restrict_
 
 // ---- launch ---------------------------------------------------------------
 enum TileId { T256 = 0, T128 = 1, T64x128 = 2, T64 = 3, S64 = 4, S32 = 5, T128S = 6,
-              P128 = 7, W256 = 8, P64 = 9, P128x64 = 10, P64x128 = 11, NUM_TILES = 12 };
+              P128 = 7, W256 = 8, P64 = 9, P128x64 = 10, P64x128 = 11, S16 = 12, NUM_TILES = 13 };
 
 template <int AMODE, bool NORM, int EPI, int ACT>
 void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
@@ -1516,6 +1530,9 @@ void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
           hipLaunchKernelGGL((gemm_wide_kernel<AMODE, NORM, EPI, ACT, false>), grid, dim3(256), 0, s, p);
       }
       break;
+    case S16:
+      hipLaunchKernelGGL((skinny_kernel<16, AMODE, NORM, EPI, ACT>), grid, dim3(SK_WAVES * 64), 0, s, p);
+      break;
     default:
       if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
         hipLaunchKernelGGL((skinny_kernel<32, AMODE, NORM, EPI, ACT>), grid, dim3(SK_WAVES * 64), 0, s, p);
@@ -1546,6 +1563,7 @@ TileCfg tile_dims(TileId id) {
     case T64x128: return {T64x128, 64, 128};
     case T64: return {T64, 64, 64};
     case S64: return {S64, 64, 64};
+    case S16: return {S16, 64, 16};
     default: return {S32, 64, 32};
   }
 }
@@ -1567,7 +1585,20 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok) {
     return tile_dims((TileId)g_force_tile);
   }
   if (M <= kSkinnyMaxM) {
-    if (!paired && tiles(64, 64) < kNumCU / 2) return {S32, 64, 32};
+    // measured on MI355X (batch-1 expert and prefix shapes): each workgroup
+    // pulls the whole A k-range, so narrower tiles spread the weight bytes
+    // over more CUs at little extra cost while the grid still fits the chip.
+    // 16 columns beat 32 / 64: expert O 50x720x960 7.6 -> 6.5 us; down
+    // 50x720x2048 with 4 splits 9.3 -> 8.4; prefix O 241x960x960 8.4 -> 7.2;
+    // paired (8 columns + their partners, bit-identical results) expert
+    // norm + QKV + RoPE 50x1600x720 7.7 -> 6.2, norm + gate|up 50x4096x720
+    // 7.7 -> 6.4.  Not past one tile per CU (prefix norm + QKV 241x1600x960:
+    // 11.6 -> 15.0 us), nor for long K on grids over half the chip, where the
+    // 32-column tile's split wins (prefix down 241x960x2560: 13.5 vs 14.0 us).
+    const long t16 = tiles(64, 16);
+    if (paired) return t16 <= kNumCU ? TileCfg{S16, 64, 16} : TileCfg{S64, 64, 64};
+    if (t16 <= kNumCU / 2 || (K < 1536 && t16 <= kNumCU)) return {S16, 64, 16};
+    if (tiles(64, 64) < kNumCU / 2) return {S32, 64, 32};
     return {S64, 64, 64};
   }
   // measured on MI355X: 128x128 tiles win once the grid has ~4 waves of
@@ -1704,7 +1735,7 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
     p.tiles_n = gn;
     grid = dim3(min(gm * gn, kNumCU), 1, 1);
   }
-  if (t.id == S32 || t.id == S64) {
+  if (t.id == S32 || t.id == S64 || t.id == S16) {
     const int S = pick_split(gm * gn, p.K, t.bm, t.bn);
     const SplitWs* w = S > 1 ? split_ws(s) : nullptr;
     if (w) {
