@@ -75,7 +75,7 @@ def test_rmsnorm_strided_rows(ops):
     assert (out[:, 960:] == 0).all()
 
 
-@pytest.mark.parametrize("rows,cols", [(1024, 768), (4, 768), (7, 128)])
+@pytest.mark.parametrize("rows,cols", [(1024, 768), (4, 768), (7, 128), (9, 768), (5, 1536)])
 def test_layernorm(ops, rows, cols):
     g = gen(3)
     x = (torch.randn(rows, cols, generator=g) * 2 + 0.5).to(BF16)

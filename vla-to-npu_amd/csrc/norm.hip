@@ -51,35 +51,53 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16* __restrict__ x
   }
 }
 
+// Sum over the LPR lanes of each row group (LPR = 64: the whole wave; 32:
+// each half separately).
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+#pragma unroll
+  for (int o = LPR / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, SVLA_WAVE);
+  return v;
+}
+
 // BLK: y is slab-blocked, element (row, c) at (c / 32) * rows * 32 + row * 32 +
 // c % 32 (the A layout the 256x256 GEMM streams as contiguous kilobytes); each
 // lane's 16-byte chunk stays inside one 64-byte slab row.
-template <bool BLK>
+// RPW rows per wave: 2 for cols <= 1024, a 32-lane half per row, so that every
+// lane holds chunks of a 768-wide row and, slab-blocked, the two halves' stores
+// of one instruction fill whole 128-byte lines (rows 2j and 2j + 1 of a slab
+// are adjacent); 1 (the whole wave) for wider rows.
+template <bool BLK, int RPW>
 __global__ __launch_bounds__(256) void layernorm_kernel(const bf16* __restrict__ x, long ldx,
                                                         const bf16* __restrict__ gmm,
                                                         const bf16* __restrict__ bta,
                                                         bf16* __restrict__ y, long ldy, int rows,
                                                         int cols, float eps) {
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const bf16* xr = x + row * ldx;
+  constexpr int LPR = 64 / RPW;  // lanes per row
+  const int lane = threadIdx.x & 63, sub = lane % LPR;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+  if (row0 >= rows) return;  // wave-uniform
+  // a second row past the end loads the last row (all lanes take part in the
+  // shuffles) and stores nothing
+  const int row = row0 + lane / LPR;
+  const bool live = row < rows;
+  const bf16* xr = x + (long)min(row, rows - 1) * ldx;
   bf16x8 v[MAXC];
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {
-    const int c = (lane + i * 64) * 8;
+    const int c = (sub + i * LPR) * 8;
     if (c < cols) {
       v[i] = ld8(xr + c);
 #pragma unroll
       for (int j = 0; j < 8; ++j) s += bf2f(v[i][j]);
     }
   }
-  const float mean = wave_sum(s) / (float)cols;
+  const float mean = row_sum<LPR>(s) / (float)cols;
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {
-    const int c = (lane + i * 64) * 8;
+    const int c = (sub + i * LPR) * 8;
     if (c < cols) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -88,11 +106,12 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const bf16* __restrict__
       }
     }
   }
-  const float rstd = 1.0f / sqrtf(wave_sum(ss) / (float)cols + eps);
-  bf16* yr = y + row * ldy;
+  const float rstd = 1.0f / sqrtf(row_sum<LPR>(ss) / (float)cols + eps);
+  if (!live) return;
+  bf16* yr = y + (long)row * ldy;
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {
-    const int c = (lane + i * 64) * 8;
+    const int c = (sub + i * LPR) * 8;
     if (c < cols) {
       const bf16x8 gv = ld8(gmm + c);
       bf16x8 bv = bta ? ld8(bta + c) : bf16x8{};
@@ -106,6 +125,20 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const bf16* __restrict__
         st8(yr + c, o);
     }
   }
+}
+
+template <bool BLK>
+void launch_layernorm(const void* x, int ldx, const void* gamma, const void* beta, void* y,
+                      long ldy, int rows, int cols, float eps, hipStream_t stream) {
+  const int rpw = cols <= 4 * 8 * 32 ? 2 : 1;
+  const dim3 grid((rows + 4 * rpw - 1) / (4 * rpw));
+  auto args = [&](auto kern) {
+    hipLaunchKernelGGL(kern, grid, dim3(256), 0, stream, static_cast<const bf16*>(x), (long)ldx,
+                       static_cast<const bf16*>(gamma), static_cast<const bf16*>(beta),
+                       static_cast<bf16*>(y), ldy, rows, cols, eps);
+  };
+  if (rpw == 2) args(layernorm_kernel<BLK, 2>);
+  else args(layernorm_kernel<BLK, 1>);
 }
 
 bool norm_args_ok(const void* x, int ldx, const void* y, int ldy, int cols) {
@@ -133,10 +166,7 @@ extern "C" int svla_layernorm_bf16(const void* x, int ldx, const void* gamma, co
     return SVLA_EINVAL;
   if (beta && !svla_aligned16(beta)) return SVLA_EINVAL;
   if (rows == 0) return SVLA_OK;
-  hipLaunchKernelGGL(layernorm_kernel<false>, dim3((rows + 3) / 4), dim3(256), 0,
-                     (hipStream_t)stream, static_cast<const bf16*>(x), (long)ldx,
-                     static_cast<const bf16*>(gamma), static_cast<const bf16*>(beta),
-                     static_cast<bf16*>(y), (long)ldy, rows, cols, eps);
+  launch_layernorm<false>(x, ldx, gamma, beta, y, ldy, rows, cols, eps, (hipStream_t)stream);
   SVLA_CHECK_LAUNCH();
   return SVLA_OK;
 }
@@ -148,10 +178,7 @@ extern "C" int svla_layernorm_blocked_bf16(const void* x, int ldx, const void* g
     return SVLA_EINVAL;
   if (beta && !svla_aligned16(beta)) return SVLA_EINVAL;
   if (rows == 0) return SVLA_OK;
-  hipLaunchKernelGGL(layernorm_kernel<true>, dim3((rows + 3) / 4), dim3(256), 0,
-                     (hipStream_t)stream, static_cast<const bf16*>(x), (long)ldx,
-                     static_cast<const bf16*>(gamma), static_cast<const bf16*>(beta),
-                     static_cast<bf16*>(y), 0L, rows, cols, eps);
+  launch_layernorm<true>(x, ldx, gamma, beta, y, 0L, rows, cols, eps, (hipStream_t)stream);
   SVLA_CHECK_LAUNCH();
   return SVLA_OK;
 }
