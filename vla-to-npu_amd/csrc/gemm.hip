@@ -1607,7 +1607,10 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok) {
   // wide tile beats the 128x128 pipeline from K = 512 (K = 768 + GELU: 675 vs
   // 752 us; K = 3072: 1603 vs 2285 us) and loses below (K = 256: 465 vs 430)
   if (wide_ok && K >= 512 && tiles(WBM, WBN) >= 2 * kNumCU) return tile_dims(W256);
-  if (M >= 4096 || tiles(128, 128) >= 4 * kNumCU) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
+  // from M = 3072 (the batch-1 ViT, 3 images) too, measured on MI355X: up
+  // 3072x3072x768 + GELU 38.1 -> 35.0 us, down 3072x768x3072 42.7 -> 34.1 us,
+  // QKV and O within 0.4 us
+  if (M >= 3072 || tiles(128, 128) >= 4 * kNumCU) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
   // mid-size (the batched expert, M = 1600), measured on MI355X: with at least
   // one 128x128 tile per CU the 32x32-MFMA register-staged 128x128 kernel wins
   // (gate|up 1600x4096x720: 19 us vs 34 us on 64x64); below that the 64x64

@@ -105,6 +105,10 @@ class SmolVLAEngine:
         self.h_time = z(M, e.hidden)
         self.ex = z(M, e.hidden)
         self.ebufs = layers.Buffers(dev)
+        # the time part of the action-time MLP input depends only on the
+        # weights and the fixed Euler schedule: computed once, like the RoPE
+        # tables, not per chunk
+        self.time_bias(self.schedule())
         # materialise every lazily-named buffer before any capture
         self._forward()
         torch.cuda.synchronize(dev)
@@ -149,9 +153,19 @@ class SmolVLAEngine:
             layers.cross_kv(kv[:, qd:qd + kvd], kv[:, qd + kvd:], self.expert[i], out_k=ck,
                             out_v=cv)
 
+    def schedule(self):
+        """Euler times t_s = 1, 1 + dt, ... (dt = -1 / num_steps)."""
+        dt = -1.0 / self.cfg.num_steps
+        ts, t = [], 1.0
+        for _ in range(self.cfg.num_steps):
+            ts.append(t)
+            t = t + dt
+        return ts
+
     def time_bias(self, ts):
         """Time part of the action-time MLP input for every Euler step, hoisted
-        out of the loop (it depends on t only): tbias[s] = temb(t_s) @ W_time_in[H:]
+        out of the chunk (it depends on t only, and the schedule is fixed; the
+        engine computes it once at set-up): tbias[s] = temb(t_s) @ W_time_in[H:]
         + b_time_in, kept in fp32 so that the per-step GEMM rounds once as the
         concatenated projection does."""
         e = self.cfg.expert
@@ -188,11 +202,6 @@ class SmolVLAEngine:
         self.x_t.copy_(self.in_noise.view(-1, cfg.action_dim))
         ops.f32_to_bf16(self.x_t, out=self.x_bf)
         dt = -1.0 / cfg.num_steps
-        ts, t = [], 1.0
-        for _ in range(cfg.num_steps):
-            ts.append(t)
-            t = t + dt
-        self.time_bias(ts)
         for s in range(cfg.num_steps):
             self.expert_step(s, dt)
 
