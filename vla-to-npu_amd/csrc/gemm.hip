@@ -1595,8 +1595,14 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok) {
     // 7.7 -> 6.4.  Not past one tile per CU (prefix norm + QKV 241x1600x960:
     // 11.6 -> 15.0 us), nor for long K on grids over half the chip, where the
     // 32-column tile's split wins (prefix down 241x960x2560: 13.5 vs 14.0 us).
+    // Paired problems past that go to the 64x64 LDS-DMA pipeline (prefix
+    // norm + gate|up 241x5120x960: 21.5 -> 11.8 us on the 64-column skinny
+    // tile; norm + QKV + RoPE 241x1600x960: 12.0 -> 10.1 us).
     const long t16 = tiles(64, 16);
-    if (paired) return t16 <= kNumCU ? TileCfg{S16, 64, 16} : TileCfg{S64, 64, 64};
+    if (paired) {
+      if (t16 <= kNumCU) return {S16, 64, 16};
+      return pipe_ok ? tile_dims(P64) : TileCfg{S64, 64, 64};
+    }
     if (t16 <= kNumCU / 2 || (K < 1536 && t16 <= kNumCU)) return {S16, 64, 16};
     if (tiles(64, 64) < kNumCU / 2) return {S32, 64, 32};
     return {S64, 64, 64};
