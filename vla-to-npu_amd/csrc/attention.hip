@@ -4,8 +4,12 @@
 // P.V GEMM  (vla/text_encoder_bf16.py:502-526, vla/vision_block_bf16.py:325-367,
 // vla/action_expert_bf16.py:689-713, 764-787) with one kernel per call.
 // Numerics follow the torch modules (vla/text_encoder_bf16.py:117-126):
-// scores and softmax statistics in fp32, probabilities rounded to bf16 before
-// the P.V product, fp32 accumulation, bf16 output.
+// scores and the running maximum in fp32, probabilities rounded to bf16 before
+// the P.V product, fp32 accumulation, bf16 output.  The softmax denominator is
+// the fp32 sum of the same bf16-rounded probabilities that multiply V
+// (accumulated on the MFMA), so the normalised weights sum to 1 exactly as
+// used; torch sums the unrounded fp32 values, a difference below bf16's
+// rounding of the output.
 //
 // Work decomposition: one workgroup = 128 query rows of one query head
 // (4 waves x 32 rows); K/V blocks of 64 keys stream through a 3-stage LDS
@@ -59,14 +63,6 @@ __device__ __forceinline__ float max_xor16(float x) {
 __device__ __forceinline__ float max_xor32(float x) {
   const u32x2_t r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float sum_xor16(float x) {
-  const u32x2_t r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-__device__ __forceinline__ float sum_xor32(float x) {
-  const u32x2_t r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 typedef __attribute__((address_space(3))) v4i16* lds_v4i16_ptr;
 
@@ -168,16 +164,23 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
     for (int ks = 0; ks < 2; ++ks) qf[qt][ks] = ld8(qb + (long)qi * p.ldq + ks * 32 + grp * 8);
   }
 
-  f32x4 o[2][4];
+  // o[qt][0..3]: O^T tiles (head dims 16 t .. 16 t + 15); o[qt][4]: the
+  // softmax denominator, accumulated by the MFMA with an all-ones V^T operand
+  // (every row of that tile holds sum_k bf16(p[q, k]) for the lane's query q),
+  // so it is rescaled with the outputs and needs no VALU sums or shuffles
+  f32x4 o[2][5];
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-    for (int t = 0; t < 4; ++t) o[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < 5; ++t) o[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 ones;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = f2bf(1.0f);
   int klim[2];  // per query tile: this lane's query sees keys < klim
 #pragma unroll
   for (int qt = 0; qt < 2; ++qt)
     klim[qt] = key_limit(p.mask_kind, qw + qt * 16 + col, p.sk, p.prefix_len);
-  float m_run[2] = {-INFINITY, -INFINITY}, l_run[2] = {0.f, 0.f};
+  float m_run[2] = {-INFINITY, -INFINITY};
   const float c = p.scale_log2;
 
   auto compute = [&](auto SI, int blk) {
@@ -230,23 +233,17 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
       if (__builtin_amdgcn_ballot_w64(grow)) {
         const float m_new = fmaxf(m_run[qt], mx);
         const float alpha = m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
-        l_run[qt] *= alpha;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) o[qt][t] *= alpha;
+        for (int t = 0; t < 5; ++t) o[qt][t] *= alpha;
         m_run[qt] = m_new;
       }
       const float mc = (m_run[qt] == -INFINITY ? 0.f : m_run[qt]) * c;  // fully-masked-so-far guard
-      float psum = 0.f;
 #pragma unroll
       for (int ts = 0; ts < 4; ++ts)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[ts][qt][i], c, -mc));
-          psum += e;
-          pf[qt][ts >> 1][(ts & 1) * 4 + i] = f2bf(e);
-        }
-      psum = sum_xor32(sum_xor16(psum));
-      l_run[qt] += psum;
+        for (int i = 0; i < 4; ++i)
+          pf[qt][ts >> 1][(ts & 1) * 4 + i] =
+              f2bf(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[ts][qt][i], c, -mc)));
     }
     // O^T[d, q] += V^T[d, keys] . P^T[keys, q]; V^T fragments shared by both query tiles
 #pragma unroll
@@ -261,6 +258,9 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
         for (int qt = 0; qt < 2; ++qt)
           o[qt][td] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qt][kk], o[qt][td], 0, 0, 0);
       }
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt)
+        o[qt][4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[qt][kk], o[qt][4], 0, 0, 0);
     }
   };
 
@@ -296,7 +296,8 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
   for (int qt = 0; qt < 2; ++qt) {
     const int qi = qw + qt * 16 + col;
     if (qi >= p.sq) continue;
-    const float inv = l_run[qt] > 0.f ? 1.0f / l_run[qt] : 0.f;
+    const float l = o[qt][4][0];
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
     bf16* orow = p.o + b * p.o_bs + (long)qi * p.ldo + h * D;
 #pragma unroll
     for (int td = 0; td < 4; ++td) {
