@@ -46,3 +46,21 @@ def test_ops_refuse_cpu_tensors():
     x = torch.zeros(4, 64, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU tensors"):
         ops.rmsnorm(x, torch.ones(64, dtype=torch.bfloat16), 1e-5)
+
+
+@pytest.mark.parametrize("m,n,k,tile", [
+    (50, 720, 960, 12),      # batch-1 expert O: 16-column skinny tile
+    (50, 720, 2048, 12),     # batch-1 expert down (split over workgroups)
+    (241, 960, 960, 12),     # batch-1 prefix O
+    (241, 960, 2560, 5),     # batch-1 prefix down: 32-column tile, split 2
+    (3072, 768, 3072, 7),    # batch-1 ViT down: 128x128 LDS-DMA pipeline
+    (3072, 3072, 768, 7),    # batch-1 ViT up
+    (1600, 720, 960, 10),    # batch-32 expert O: 128x64 pipeline
+    (98304, 3072, 768, 8),   # batch-32 ViT up: persistent 256x256 tile
+])
+def test_gemm_tile_choice(m, n, k, tile):
+    """The automatic GEMM tile choice (a host-only query, no GPU call) for
+    the shapes the engine runs; numbering as svla_gemm_set_tile."""
+    from smolvla import _lib
+    lib = _lib.load()
+    assert lib.svla_gemm_tile_choice(m, n, k, 0) == tile
