@@ -177,9 +177,15 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
 #pragma unroll
   for (int j = 0; j < 8; ++j) ones[j] = f2bf(1.0f);
   int klim[2];  // per query tile: this lane's query sees keys < klim
+  int kmin[2];  // ... and the smallest limit over the wave (wave-uniform)
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int qt = 0; qt < 2; ++qt) {
     klim[qt] = key_limit(p.mask_kind, qw + qt * 16 + col, p.sk, p.prefix_len);
+    int t = klim[qt];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) t = min(t, __shfl_xor(t, o, 64));
+    kmin[qt] = __builtin_amdgcn_readfirstlane(t);
+  }
   float m_run[2] = {-INFINITY, -INFINITY};
   const float c = p.scale_log2;
 
@@ -209,7 +215,8 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
     bf16x8 pf[2][2];
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) {
-      if constexpr (!FULL) {
+      // only a block reaching past some query's limit needs the mask
+      if (!FULL && k0 + BKEY > kmin[qt]) {
 #pragma unroll
         for (int ts = 0; ts < 4; ++ts)
 #pragma unroll
