@@ -56,6 +56,7 @@ def test_ops_refuse_cpu_tensors():
     (3072, 768, 3072, 7),    # batch-1 ViT down: 128x128 LDS-DMA pipeline
     (3072, 3072, 768, 7),    # batch-1 ViT up
     (1600, 720, 960, 10),    # batch-32 expert O: 128x64 pipeline
+    (7712, 960, 2560, 1),    # batch-32 prefix down: register-staged 128x128
     (98304, 3072, 768, 8),   # batch-32 ViT up: persistent 256x256 tile
 ])
 def test_gemm_tile_choice(m, n, k, tile):

@@ -1569,7 +1569,7 @@ TileCfg tile_dims(TileId id) {
 }
 
 // `plain`: dense A, no fused norm, plain store epilogue (the wide kernel's scope)
-TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok) {
+TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, bool dense) {
   auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
   const bool paired = epi == EPI_ROPE || epi == EPI_SILU;
   const bool pipe_ok = K >= PBK;  // the pipelined kernels need one full K step
@@ -1613,6 +1613,11 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok) {
   // wide tile beats the 128x128 pipeline from K = 512 (K = 768 + GELU: 675 vs
   // 752 us; K = 3072: 1603 vs 2285 us) and loses below (K = 256: 465 vs 430)
   if (wide_ok && K >= 512 && tiles(WBM, WBN) >= 2 * kNumCU) return tile_dims(W256);
+  // dense A from M = 4096 (the batch-32 prefix, 7712 rows), measured on
+  // MI355X: the register-staged 128x128 kernel beats the pipeline -- gate|up
+  // + SiLU 114.5 -> 104.3 us, down 60.9 -> 57.7, QKV + RoPE 53.4 -> 52.1, O
+  // 31.5 -> 30.3; the gathers (patch embedding, connector) keep the pipeline
+  if (dense && M >= 4096) return tile_dims(T128);
   // from M = 3072 (the batch-1 ViT, 3 images) too, measured on MI355X: up
   // 3072x3072x768 + GELU 38.1 -> 35.0 us, down 3072x768x3072 42.7 -> 34.1 us,
   // QKV and O within 0.4 us
@@ -1735,7 +1740,7 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
       AMODE == A_DENSE && !p.norm_w && epi == EPI_STORE && !p.rowadd && p.c_rpg <= 0;
   const bool wide_rows_ok = !p.out_f32 && p.N % 8 == 0 && p.ldc % 8 == 0 &&
                             (!p.res || (p.ldr % 8 == 0 && svla_aligned16(p.res)));
-  const TileCfg t = pick_tile(p.M, p.N, p.K, epi, plain, wide_rows_ok);
+  const TileCfg t = pick_tile(p.M, p.N, p.K, epi, plain, wide_rows_ok, AMODE == A_DENSE);
   if (p.norm_w && p.K > 2048) return SVLA_EINVAL;  // row statistics keep <= 2048 per row
   const int gm = (p.M + t.bm - 1) / t.bm, gn = (p.N + t.bn - 1) / t.bn;
   dim3 grid(gn, gm, 1);
@@ -1790,7 +1795,7 @@ int svla_gemm_set_tile(int tile) {
 int svla_gemm_tile_choice(int m, int n, int k, int act) {
   if (m <= 0 || n <= 0 || k <= 0 || act < 0 || act > SVLA_ACT_SILU) return SVLA_EINVAL;
   (void)act;  // the choice depends on the epilogue kind, not on the activation
-  return (int)pick_tile(m, n, k, EPI_STORE, true, n % 8 == 0).id;
+  return (int)pick_tile(m, n, k, EPI_STORE, true, n % 8 == 0, true).id;
 }
 
 int svla_gemm_set_split(int splits) {
