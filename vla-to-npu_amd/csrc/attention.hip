@@ -282,15 +282,22 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
   __builtin_amdgcn_s_waitcnt(0xF70);
   issue(I0{}, 0);
   issue(I1{}, 1);
+  // masked / ragged kernel (short key ranges: the expert's 50 or 241 keys):
+  // after the last block, leave at once (nb is uniform across the
+  // workgroup), with no further refills of never-read blocks and no further
+  // barrier rounds.  (The same exits in the FULL kernel measured 6-7% slower
+  // on the ViT's 16-block loop, so that loop keeps its original form.)
   for (int blk = 0; blk < nb; blk += 3) {
     __builtin_amdgcn_s_waitcnt(kWaitOne);
     __builtin_amdgcn_s_barrier();
     issue(I2{}, blk + 2);
     compute(I0{}, blk);
+    if (!FULL && blk + 1 >= nb) break;
     __builtin_amdgcn_s_waitcnt(kWaitOne);
     __builtin_amdgcn_s_barrier();
     issue(I0{}, blk + 3);
     if (blk + 1 < nb) compute(I1{}, blk + 1);
+    if (!FULL && blk + 2 >= nb) break;
     __builtin_amdgcn_s_waitcnt(kWaitOne);
     __builtin_amdgcn_s_barrier();
     issue(I1{}, blk + 4);
