@@ -26,6 +26,17 @@ time_embedding               closed form sin/cos; sin^2+cos^2 = 1
 masked_softmax_rows          the reference test's own mask loop
 smolvla_chunk                Euler loop with a constant velocity (closed form);
                              batch independence
+is_cross                     layer parity of vla/vla.py:204-211 (SKIP = 2)
+expert_input                 float64 closed form; each half of W_time_in zeroed
+                             in turn (the output then ignores x, or t)
+build_prefix                 a distinct constant per source, checked row by row
+                             (the [cameras | language | state] order, vla/vla.py:326)
+cross_kv                     float64 projection of the same layer's K/V
+_cross_with_projected        equals expert_cross_block (itself brute-forced)
+expert_output                float64 RMSNorm then matmul
+expert_velocity              zero layer weights (identity blocks) closed form;
+                             one live cross layer with Wq = 0 (uniform attention
+                             over that layer's projected V)
 ===========================  ===================================================
 """
 
@@ -464,3 +475,199 @@ def test_chunk_batch_independence():
     assert torch.allclose(both[1:], one, atol=1e-6)
     assert both.shape == (2, cfg.chunk, cfg.action_dim)
     assert torch.isfinite(both).all()
+
+
+# --------------------------------------------------------------------------
+# Wiring of the BASELINE-only pieces (absent from the reference, whose whole
+# composition is vla/vla.py:194-222 and :326).  Each pin below is a closed form
+# that a plausible wiring mistake (swapped concat or weight half, another token
+# order, the wrong cross layer or K/V source, a dropped residual) fails.
+def _small_fp32(seed=0):
+    cfg = small_config()
+    return cfg, to32(smolvla_params(cfg, seed=seed, norm_init="random"))
+
+
+def _d(t):
+    return t.double()
+
+
+def test_is_cross_layer_parity():
+    # vla/vla.py:79, 204-211: layer i self-attends when i % SKIP == 0 (SKIP = 2)
+    cfg = SmolVLAConfig()
+    assert [cfg.is_cross(i) for i in range(cfg.expert_layers)] == [i % 2 == 1 for i in range(16)]
+    cfg_s = small_config()
+    P = smolvla_params(cfg_s, seed=0)
+    for i, lp in enumerate(P["expert"]):
+        assert ("Wk_cross" in lp) == (i % 2 == 1)
+
+
+def test_expert_input_halves_of_time_in():
+    """time_in multiplies concat([action_in(x), temb(t)]): rows [0, H) of
+    W_time_in see the action embedding, rows [H, 2H) the time embedding."""
+    cfg, P = _small_fp32(1)
+    io = P["expert_io"]
+    H = cfg.expert.hidden
+    g = torch.Generator().manual_seed(3)
+    x1 = torch.randn(2, cfg.chunk, cfg.action_dim, generator=g)
+    x2 = torch.randn(2, cfg.chunk, cfg.action_dim, generator=g)
+
+    def closed(x, t, w_tin):
+        a = _d(x) @ _d(io["W_action_in"]) + _d(io["b_action_in"])
+        k = torch.arange(H // 2, dtype=F64)
+        period = 4e-3 * (4.0 / 4e-3) ** (k / (H // 2 - 1))
+        ang = 2 * math.pi * float(torch.tensor(t, dtype=F32)) / period
+        te = torch.cat([torch.sin(ang), torch.cos(ang)])[None, None, :].expand(*a.shape[:2], H)
+        h = a @ _d(w_tin[:H]) + te @ _d(w_tin[H:]) + _d(io["b_time_in"])
+        h = h * torch.sigmoid(h)
+        return h @ _d(io["W_time_out"]) + _d(io["b_time_out"])
+
+    # the full projection against the closed form
+    for x, t in ((x1, 1.0), (x2, 0.3)):
+        got = ref.expert_input(x, t, P, cfg)
+        assert torch.allclose(_d(got), closed(x, t, io["W_time_in"]), atol=1e-4)
+    # action half zeroed: the result depends on t only
+    Pa = tree_map(lambda t: t.clone(), P)
+    Pa["expert_io"]["W_time_in"][:H] = 0
+    ya1, ya2 = ref.expert_input(x1, 0.7, Pa, cfg), ref.expert_input(x2, 0.7, Pa, cfg)
+    assert torch.equal(ya1, ya2)
+    assert not torch.allclose(ya1, ref.expert_input(x1, 0.2, Pa, cfg), atol=1e-3)
+    assert torch.allclose(_d(ya1), closed(x1, 0.7, Pa["expert_io"]["W_time_in"]), atol=1e-4)
+    # time half zeroed: the result depends on x only
+    Pt = tree_map(lambda t: t.clone(), P)
+    Pt["expert_io"]["W_time_in"][H:] = 0
+    yt1, yt2 = ref.expert_input(x1, 0.7, Pt, cfg), ref.expert_input(x1, 0.2, Pt, cfg)
+    assert torch.equal(yt1, yt2)
+    assert not torch.allclose(yt1, ref.expert_input(x2, 0.7, Pt, cfg), atol=1e-3)
+    assert torch.allclose(_d(yt1), closed(x1, 0.7, Pt["expert_io"]["W_time_in"]), atol=1e-4)
+
+
+def test_build_prefix_token_order():
+    """[camera 0 | camera 1 | ... | language | state] per sample (vla/vla.py:326),
+    each source written as a distinct constant so every row names its source."""
+    cfg = small_config()
+    P = to32(smolvla_params(cfg, seed=0))
+    B, C = 2, cfg.n_cameras
+    N, E = cfg.vit.tokens, cfg.vit.hidden
+    K = E * cfg.pixel_shuffle ** 2
+    H = cfg.decoder.hidden
+    it = cfg.image_tokens
+    vis = torch.empty(B, C, N, E)
+    for b in range(B):
+        for c in range(C):
+            vis[b, c] = 1.0 + c + 10.0 * b          # connector output = mean = this value
+    P["connector"]["W"] = torch.full((K, H), 1.0 / K)
+    ids = torch.stack([torch.arange(cfg.lang_tokens) + 100 * b for b in range(B)])
+    P["embed"] = torch.arange(cfg.vocab, dtype=F32)[:, None].expand(cfg.vocab, H).contiguous()
+    state = torch.ones(B, cfg.state_dim)
+    P["state"]["W"] = torch.full((cfg.state_dim, H), -7.0 / cfg.state_dim)
+    pre = ref.build_prefix(vis, ids, state, P, cfg)
+    assert pre.shape == (B, cfg.prefix_len, H)
+    sq = math.sqrt(H)
+    for b in range(B):
+        for c in range(C):
+            rows = pre[b, c * it:(c + 1) * it]
+            assert torch.allclose(rows, torch.full_like(rows, 1.0 + c + 10.0 * b), atol=1e-4)
+        lang = pre[b, C * it:C * it + cfg.lang_tokens, 0]
+        want = (torch.arange(cfg.lang_tokens, dtype=F64) + 100 * b) * sq
+        assert torch.allclose(_d(lang), want, rtol=1e-6)
+        assert torch.allclose(pre[b, -1], torch.full((H,), -7.0), atol=1e-4)
+    assert cfg.prefix_len == C * it + cfg.lang_tokens + 1
+
+
+def test_cross_kv_uses_the_same_layer():
+    """cross_kv projects layer i's prefix K/V for every cross layer i, no other
+    (vla/vla.py:207-211: text_k/text_v of VLM layer i feed expert layer i)."""
+    cfg, P = _small_fp32(2)
+    L, d = cfg.prefix_len, cfg.decoder
+    g = torch.Generator().manual_seed(4)
+    kv = [(torch.randn(1, L, d.kv_dim, generator=g), torch.randn(1, L, d.kv_dim, generator=g))
+          for _ in range(cfg.prefix_layers)]
+    out = ref.cross_kv(kv, P, cfg)
+    assert sorted(out) == [i for i in range(cfg.expert_layers) if i % 2 == 1]
+    for i, (k, v) in out.items():
+        lp = P["expert"][i]
+        assert torch.allclose(_d(k), _d(kv[i][0]) @ _d(lp["Wk_cross"]), atol=1e-5)
+        assert torch.allclose(_d(v), _d(kv[i][1]) @ _d(lp["Wv_cross"]), atol=1e-5)
+
+
+def test_cross_with_projected_equals_cross_block(fp32_probs):
+    """The cross layer on K/V projected ahead of time is the reference cross
+    block (vla/action_expert_bf16.py:163-207) on the raw prefix K/V."""
+    cfg = DecoderConfig(hidden=144, inter=192, n_q_heads=3, n_kv_heads=1)
+    p = to32(expert_cross_layer_params(_Gen(13, norm_init="random"), cfg, 64))
+    g = torch.Generator().manual_seed(14)
+    x = torch.randn(2, 9, 144, generator=g)
+    tk, tv = torch.randn(2, 17, 64, generator=g), torch.randn(2, 17, 64, generator=g)
+    want = ref.expert_cross_block(x, tk, tv, p, cfg)
+    got = ref._cross_with_projected(x, tk @ p["Wk_cross"], tv @ p["Wv_cross"], p, cfg)
+    assert torch.allclose(got, want, atol=1e-5)
+    # and in bf16, as the chunk runs it
+    pb = tree_map(lambda t: t.to(BF16), p)
+    xb, tkb, tvb = x.to(BF16), tk.to(BF16), tv.to(BF16)
+    want_b = ref.expert_cross_block(xb, tkb, tvb, pb, cfg)
+    got_b = ref._cross_with_projected(xb, ref.linear(tkb, pb["Wk_cross"]),
+                                      ref.linear(tvb, pb["Wv_cross"]), pb, cfg)
+    assert torch.equal(got_b, want_b)
+
+
+def test_expert_output_closed_form():
+    """Final RMSNorm then the action projection (vla/vla.py:218-222, 506-516)."""
+    cfg, P = _small_fp32(5)
+    io = P["expert_io"]
+    h = torch.randn(2, cfg.chunk, cfg.expert.hidden, generator=torch.Generator().manual_seed(6))
+    hd = _d(h)
+    want = hd / torch.sqrt(hd.pow(2).mean(-1, keepdim=True) + cfg.expert.rms_eps)
+    want = (want * _d(io["W_exp_norm"])) @ _d(io["W_action_out"])
+    got = ref.expert_output(h, P, cfg)
+    assert got.shape == (2, cfg.chunk, cfg.action_dim)
+    assert torch.allclose(_d(got), want, atol=1e-4)
+
+
+def _zero_layers(P):
+    for lp in P["expert"]:
+        for k in ("Wq", "Wk", "Wv", "Wo", "W_gate", "W_up", "W_down"):
+            if k in lp:
+                lp[k] = torch.zeros_like(lp[k])
+
+
+def test_expert_velocity_zero_layers_closed_form(fp32_probs):
+    """With every layer's projections zero, each block is the identity (its
+    residuals carry x through), so v = expert_output(expert_input(x, t))."""
+    cfg, P = _small_fp32(7)
+    _zero_layers(P)
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(1, cfg.chunk, cfg.action_dim, generator=g)
+    L, kvd = cfg.prefix_len, cfg.expert.kv_dim
+    ckv = {i: (torch.randn(1, L, kvd, generator=g), torch.randn(1, L, kvd, generator=g))
+           for i in range(cfg.expert_layers) if cfg.is_cross(i)}
+    got = ref.expert_velocity(x, 0.4, ckv, P, cfg)
+    want = ref.expert_output(ref.expert_input(x, 0.4, P, cfg), P, cfg)
+    assert torch.allclose(got, want, atol=1e-5)
+
+
+def test_expert_velocity_routes_cross_layer_kv(fp32_probs):
+    """Only cross layer i is live, with Wq = 0 (uniform attention) and no MLP:
+    h = h0 + mean_keys(V_i) . Wo_i, V_i being layer i's projected cross V.  A
+    velocity that reads another layer's K/V, treats layer i as a self layer or
+    drops the residual fails."""
+    cfg, P = _small_fp32(9)
+    e = cfg.expert
+    _zero_layers(P)
+    g = torch.Generator().manual_seed(10)
+    L = cfg.prefix_len
+    ckv = {i: (torch.randn(1, L, e.kv_dim, generator=g),
+               torch.randn(1, L, e.kv_dim, generator=g) + i)
+           for i in range(cfg.expert_layers) if cfg.is_cross(i)}
+    x = torch.randn(1, cfg.chunk, cfg.action_dim, generator=g)
+    h0 = _d(ref.expert_input(x, 0.9, P, cfg))
+    for live in ckv:
+        Q = tree_map(lambda t: t.clone(), P)
+        Q["expert"][live]["Wo"] = torch.randn(e.q_dim, e.hidden, generator=g) * 0.1
+        got = ref.expert_velocity(x, 0.9, ckv, Q, cfg)
+        vmean = _d(ckv[live][1]).mean(1)                       # [1, kv_dim]
+        grp = e.n_q_heads // e.n_kv_heads
+        ctx = torch.cat([vmean[:, (h // grp) * e.head_dim:(h // grp + 1) * e.head_dim]
+                         for h in range(e.n_q_heads)], dim=1)  # [1, q_dim]
+        h = h0 + (ctx @ _d(Q["expert"][live]["Wo"]))[:, None, :]
+        want = ref.expert_output(h.float(), Q, cfg)
+        assert torch.allclose(got, want, atol=1e-4), live
