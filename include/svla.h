@@ -144,7 +144,13 @@ int svla_slab_block_bf16(const void* x, int ldx, void* out, int rows, int k, svl
  * pipeline, 8: 256x256 5-stage LDS-DMA pipeline with 128x128 wave tiles, 9: 64x64
  * 4-stage LDS-DMA pipeline, 10: 128x64 and 11: 64x128 4-stage LDS-DMA pipelines, 12: skinny
  * 64x16), or -1 for the automatic
- * shape-based choice (default).  Process-wide; not thread-safe. */
+ * shape-based choice (default).  A forced tile that cannot serve a problem (too
+ * short a K for a pipelined tile, a paired RoPE / SiLU epilogue on a tile
+ * without one, anything but a plain dense store on the 256x256 pipeline) is
+ * replaced by the nearest tile that can, unless SVLA_TILE_STRICT is or-ed in:
+ * then such calls return SVLA_EINVAL and launch nothing.  Process-wide; not
+ * thread-safe. */
+#define SVLA_TILE_STRICT 0x100
 int svla_gemm_set_tile(int tile);
 
 /* Query: the tile configuration (numbering of svla_gemm_set_tile) that

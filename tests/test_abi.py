@@ -65,3 +65,31 @@ def test_gemm_tile_choice(m, n, k, tile):
     from smolvla import _lib
     lib = _lib.load()
     assert lib.svla_gemm_tile_choice(m, n, k, 0) == tile
+
+
+@pytest.mark.parametrize("tile,norm,rope", [
+    (8, True, False),    # 256x256 pipeline: no fused-norm kernel
+    (10, False, True),   # 128x64 pipeline: no paired RoPE epilogue
+    (5, False, True),    # 32-column skinny tile: no paired RoPE epilogue
+])
+def test_strict_forced_tile_without_kernel_is_einval(tile, norm, rope):
+    """A strictly forced tile / epilogue pair that has no kernel returns
+    SVLA_EINVAL before any launch (so this runs without a GPU: the pointers
+    are never dereferenced)."""
+    import ctypes as C
+    from smolvla import _lib
+    lib = _lib.load()
+    fake = C.c_void_p(1 << 20)           # 16-byte aligned, never touched
+    assert lib.svla_gemm_set_tile(tile | 0x100) == 0
+    try:
+        if rope:
+            rc = lib.svla_linear_rope_bf16(fake, 64, fake, 64, fake, 128, 64, 128, 64, 64, 64,
+                                           fake, fake, None, C.c_float(1e-5), None)
+        else:
+            rc = lib.svla_linear_bf16(fake, 768, fake, 768, None, None, None, 0, fake, 768, 1024,
+                                      768, 768, C.c_float(1.0), 0, 0,
+                                      fake if norm else None, C.c_float(1e-5), None)
+    finally:
+        lib.svla_gemm_set_tile(-1)
+    assert rc == -22
+    assert lib.svla_gemm_set_tile(13 | 0x100) == -22

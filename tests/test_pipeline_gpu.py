@@ -109,3 +109,49 @@ def test_batch_rows_independent(full):
     cfg, P, inputs, want, _ = full
     one = SmolVLAEngine(cfg, P, batch=1).run(*[t[1:].cuda() for t in inputs]).cpu()
     assert (one - want[1:]).abs().max().item() <= ACTION_ATOL
+
+
+def test_batch32_engine_matches_oracle_and_batch1():
+    """The engine bench.py times (config 4 at batch 32): every batch-32 kernel
+    choice (slab-blocked 256x256 ViT GEMMs, the 7712-row prefix GEMMs, the
+    1600-row expert GEMMs) composed.  Sample rows 0, 17 and 31 against the
+    oracle (stages and actions), and all 32 rows against the batch-1 engine,
+    which runs different kernels (vla/vla.py:228-338 composition)."""
+    from smolvla.pipeline import SmolVLAEngine
+    cfg = SmolVLAConfig()
+    P = smolvla_params(cfg, seed=0, norm_init="random")
+    B = 32
+    inputs = smolvla_inputs(cfg, batch=B, seed=5)
+    eng = SmolVLAEngine(cfg, P, batch=B, use_graph=True)
+    got = eng.run(*[t.cuda() for t in inputs]).cpu()
+    assert torch.isfinite(got).all()
+    rows = [0, 17, 31]
+    sub = [t[rows] for t in inputs]
+    cap = {}
+    with torch.inference_mode():
+        want = ref.smolvla_chunk(*sub, P, cfg, capture=cap)
+    err = (got[rows] - want).abs().max().item()
+    d = cfg.decoder
+    vis = eng.vit_x.view(B, cfg.n_cameras, cfg.vit.tokens, -1)[rows]
+    pairs = [("vision", vis, cap["vision"])]
+    for i in (0, cfg.prefix_layers - 1):
+        kv = eng.kv[i].view(B, cfg.prefix_len, -1)[rows]
+        k, v = cap["kv"][i]
+        pairs.append((f"K{i}", kv[:, :, d.q_dim:d.q_dim + d.kv_dim], k))
+        pairs.append((f"V{i}", kv[:, :, d.q_dim + d.kv_dim:], v))
+    worst_max = max((rel_err(g, w), n) for n, g, w in pairs)
+    worst_fro = max((fro_err(g, w), n) for n, g, w in pairs)
+    print(f"batch 32 rows {rows}: stages worst max-rel {worst_max}, fro-rel {worst_fro}; "
+          f"actions max abs {err:.3e}")
+    assert worst_max[0] <= STAGE_MAX_REL
+    assert worst_fro[0] <= STAGE_FRO_REL
+    assert err <= ACTION_ATOL
+    del eng
+    torch.cuda.empty_cache()
+    one = SmolVLAEngine(cfg, P, batch=1, use_graph=True)
+    worst = 0.0
+    for b in range(B):
+        r = one.run(*[t[b:b + 1].cuda() for t in inputs]).cpu()
+        worst = max(worst, (r - got[b:b + 1]).abs().max().item())
+    print(f"batch 32 vs batch-1 engine, all rows: max abs {worst:.3e}")
+    assert worst <= ACTION_ATOL

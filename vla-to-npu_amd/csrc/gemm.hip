@@ -1488,8 +1488,12 @@ __global__ __launch_bounds__(256) void slab_block_kernel(const bf16* __restrict_
 enum TileId { T256 = 0, T128 = 1, T64x128 = 2, T64 = 3, S64 = 4, S32 = 5, T128S = 6,
               P128 = 7, W256 = 8, P64 = 9, P128x64 = 10, P64x128 = 11, S16 = 12, NUM_TILES = 13 };
 
+// Launches tile configuration t; SVLA_EINVAL for a tile / epilogue pair that
+// has no kernel (the 128x64 pipeline and the 32-column skinny tile have no
+// paired RoPE / SiLU epilogue, the wide tile only the plain dense store), so a
+// forced or mis-routed choice fails loudly instead of leaving C unwritten.
 template <int AMODE, bool NORM, int EPI, int ACT>
-void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
+int launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
   switch (t) {
     case T256:
       hipLaunchKernelGGL((gemm_kernel<256, 256, 2, 2, 32, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
@@ -1518,6 +1522,8 @@ void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
     case P128x64:
       if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
         hipLaunchKernelGGL((gemm_pipe_kernel<128, 64, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      else
+        return SVLA_EINVAL;
       break;
     case P64x128:
       hipLaunchKernelGGL((gemm_pipe_kernel<64, 128, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
@@ -1528,15 +1534,23 @@ void launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
           hipLaunchKernelGGL((gemm_wide_kernel<AMODE, NORM, EPI, ACT, true>), grid, dim3(256), 0, s, p);
         else
           hipLaunchKernelGGL((gemm_wide_kernel<AMODE, NORM, EPI, ACT, false>), grid, dim3(256), 0, s, p);
+      } else {
+        return SVLA_EINVAL;
       }
       break;
     case S16:
       hipLaunchKernelGGL((skinny_kernel<16, AMODE, NORM, EPI, ACT>), grid, dim3(SK_WAVES * 64), 0, s, p);
       break;
-    default:
+    case S32:
       if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
         hipLaunchKernelGGL((skinny_kernel<32, AMODE, NORM, EPI, ACT>), grid, dim3(SK_WAVES * 64), 0, s, p);
+      else
+        return SVLA_EINVAL;
+      break;
+    default:
+      return SVLA_EINVAL;
   }
+  return 0;
 }
 
 constexpr int kNumCU = 256;
@@ -1547,8 +1561,11 @@ struct TileCfg {
   int bm, bn;
 };
 
-// Tuning override (svla_gemm_set_tile): -1 = automatic choice.
+// Tuning override (svla_gemm_set_tile): -1 = automatic choice.  Strict: the
+// forced tile is used as given, with no substitution for problems it cannot
+// serve (those calls then fail with SVLA_EINVAL).
 int g_force_tile = -1;
+bool g_force_strict = false;
 
 TileCfg tile_dims(TileId id) {
   switch (id) {
@@ -1576,6 +1593,7 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, b
   // whole 4-step rounds and at least 8 K steps; 16-byte row stores (N, ldc,
   // ldr multiples of 8)
   const bool wide_ok = plain && K % (4 * WBK) == 0 && K >= 8 * WBK && wide_rows_ok;
+  if (g_force_tile >= 0 && g_force_strict) return tile_dims((TileId)g_force_tile);
   if (g_force_tile >= 0 && !(paired && g_force_tile == S32)) {
     if (g_force_tile == W256 && !wide_ok) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
     if (g_force_tile == P128 && !pipe_ok) return tile_dims(T128);
@@ -1707,18 +1725,20 @@ int pick_split(int tiles, int K, int bm, int bn) {
 
 template <int AMODE, bool NORM>
 int dispatch(const GemmArgs& p, int epi, int act, TileId t, dim3 grid, hipStream_t s) {
+  int rc;
   switch (epi) {
-    case EPI_ROPE: launch_tile<AMODE, NORM, EPI_ROPE, 0>(t, grid, p, s); break;
-    case EPI_SILU: launch_tile<AMODE, NORM, EPI_SILU, 0>(t, grid, p, s); break;
-    case EPI_EULER: launch_tile<AMODE, NORM, EPI_EULER, 0>(t, grid, p, s); break;
+    case EPI_ROPE: rc = launch_tile<AMODE, NORM, EPI_ROPE, 0>(t, grid, p, s); break;
+    case EPI_SILU: rc = launch_tile<AMODE, NORM, EPI_SILU, 0>(t, grid, p, s); break;
+    case EPI_EULER: rc = launch_tile<AMODE, NORM, EPI_EULER, 0>(t, grid, p, s); break;
     default:
       switch (act) {
-        case SVLA_ACT_GELU_TANH: launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_GELU_TANH>(t, grid, p, s); break;
-        case SVLA_ACT_GELU_ERF: launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_GELU_ERF>(t, grid, p, s); break;
-        case SVLA_ACT_SILU: launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_SILU>(t, grid, p, s); break;
-        default: launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_NONE>(t, grid, p, s);
+        case SVLA_ACT_GELU_TANH: rc = launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_GELU_TANH>(t, grid, p, s); break;
+        case SVLA_ACT_GELU_ERF: rc = launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_GELU_ERF>(t, grid, p, s); break;
+        case SVLA_ACT_SILU: rc = launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_SILU>(t, grid, p, s); break;
+        default: rc = launch_tile<AMODE, NORM, EPI_STORE, SVLA_ACT_NONE>(t, grid, p, s);
       }
   }
+  if (rc) return rc;
   SVLA_CHECK_LAUNCH();
   return 0;
 }
@@ -1787,8 +1807,11 @@ extern "C" {
 int svla_version(void) { return 200; }
 
 int svla_gemm_set_tile(int tile) {
+  const bool strict = tile >= 0 && (tile & SVLA_TILE_STRICT);
+  if (strict) tile &= ~SVLA_TILE_STRICT;
   if (tile < -1 || tile >= NUM_TILES) return SVLA_EINVAL;
   g_force_tile = tile;
+  g_force_strict = strict;
   return SVLA_OK;
 }
 
