@@ -17,10 +17,19 @@
  *    K contiguous, i.e. nn.Linear's own layout).  The reference stores them
  *    [in, out] (vla/text_encoder_bf16.py:601-611); svla_pack_weight_bf16 turns
  *    one into the other on the device.
- *  - Caller owns all memory, including workspaces; the library allocates
- *    nothing per call and keeps no per-call state.  Calls are asynchronous on
- *    the given stream (NULL = default stream) and may be captured in a HIP
- *    graph (no memset / allocation inside).
+ *  - Caller owns all memory except one split-K workspace per device (skinny
+ *    GEMMs, see svla_linear_bf16), which svla_init allocates at set-up (or the
+ *    first split call outside graph capture, if svla_init was not called); the
+ *    library keeps no per-call state.  Calls are asynchronous on the given
+ *    stream (NULL = default stream) and may be captured in a HIP graph (no
+ *    memset / allocation inside).
+ *  - Concurrency: calls on one stream, and replays of graphs captured from one
+ *    stream, are ordered and bit-reproducible.  Running this library's kernels
+ *    on two or more streams of one device at the same time is NOT supported:
+ *    an experiment that ran the action expert on a second stream beside the
+ *    vision encoder and prefix (with one workspace per stream, and also with
+ *    the split turned off) produced wrong prefix rows in some runs, and the
+ *    cause was not found.  This covers concurrent engines on one device too.
  *  - Return value: 0 on success, SVLA_EINVAL for bad shapes/alignment, or a
  *    hipError_t (positive) from the launch.
  */
@@ -35,6 +44,7 @@ extern "C" {
 
 #define SVLA_OK 0
 #define SVLA_EINVAL (-22)
+#define SVLA_ENOSPC (-28) /* svla_linear_scratch_bf16: the split needs more scratch than it has */
 
 typedef void* svla_stream_t; /* hipStream_t */
 
@@ -69,6 +79,17 @@ typedef void* svla_stream_t; /* hipStream_t */
 
 /* Library version (major*10000 + minor*100 + patch). */
 int svla_version(void);
+
+/* Set-up for the CURRENT device, once per device before any graph capture
+ * (later calls return at once): allocates the split-K workspace of skinny
+ * GEMMs (16 MB of fp32 partial tiles + 4096 arrival counters, kept until the
+ * process ends), so that eager calls and calls captured into a graph split
+ * long-K problems the same way, and resolves the device address of the static
+ * scratch array of svla_linear_scratch_bf16 (allocating nothing for it),
+ * clearing its counters.  Synchronises the device.  No counterpart in the
+ * reference (its AIE modules are built per kernel by df.build at import,
+ * vla/text_encoder_bf16.py:368-392). */
+int svla_init(void);
 
 /* ---------------------------------------------------------------- norms --
  * RMSNorm, y = x * rsqrt(mean(x^2) + eps) * w, fp32 math, one bf16 rounding.
@@ -112,14 +133,35 @@ int svla_layernorm_blocked_bf16(const void* x, int ldx, const void* gamma, const
  * K % 8 == 0, N % 4 == 0, aligned.  Problems with few rows (M <= 256) split K
  * across the 8 waves of each workgroup and, when that grid is far smaller than
  * the chip, across workgroups too: the partial tiles go to a per-device
- * workspace (allocated by the library on the first such call that is not being
- * graph-captured, kept until exit) and the last workgroup of each tile sums
- * them in a fixed order.  Such calls on different streams of one device must
- * not overlap in time (svla_gemm_set_split(1) turns the split off). */
+ * workspace (allocated by svla_init, or by the first such call that is not
+ * being graph-captured; kept until exit; a split call captured before either
+ * runs unsplit) and the last workgroup of each tile sums them in a fixed
+ * order.  Calls on different streams must not overlap in time (see
+ * Concurrency above). */
 int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
                      const float* bias_f32, const void* res, int ldr, void* c, int ldc, int m,
                      int n, int k, float alpha, int act, int out_f32, const void* norm_w,
                      float norm_eps, svla_stream_t stream);
+
+/* svla_linear_bf16 that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot call hipMalloc (code under HIP graph capture
+ * before any set-up, tight serving loops, harnesses that forbid allocation).
+ * Same arguments, kernels and results as svla_linear_bf16, bit for bit (the
+ * same tile and the same K split); the split-K partial tiles of skinny
+ * problems go to a static device array instead of the allocated workspace:
+ * 4 MB of fp32 partials + 1024 arrival counters per device, held from module
+ * load until the process ends.  A call whose split needs more (more than 1024
+ * output tiles, or tiles x splits x (tile + 64) floats over 1M) returns
+ * SVLA_ENOSPC and launches nothing; problems that do not split use no scratch
+ * and have no limit.  The first call on a device (or svla_init) resolves the
+ * array's device address (hipGetSymbolAddress, no allocation) and clears its
+ * counters with a kernel on `stream`; every call leaves them at zero.  All
+ * calls on one device share the array: calls that overlap in time on one
+ * device race (see Concurrency above). */
+int svla_linear_scratch_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
+                             const float* bias_f32, const void* res, int ldr, void* c, int ldc,
+                             int m, int n, int k, float alpha, int act, int out_f32,
+                             const void* norm_w, float norm_eps, svla_stream_t stream);
 
 /* The big-problem GEMM of svla_linear_bf16 (persistent 256x256 tiles, plain
  * store epilogue: bias, fp32 bias, alpha, activation, residual) with optional

@@ -1700,6 +1700,59 @@ const SplitWs* split_ws(hipStream_t s) {
   return &w;
 }
 
+// ---- allocation-free split-K scratch (svla_linear_scratch_bf16) ------------
+// A static device array stands in for the allocated workspace: kScratchFloats
+// fp32 partial-tile slots, then kScratchTiles arrival counters (4 MB + 4 KB).
+// Every device the library runs on holds its own copy from module load until
+// the process ends.  In host code `scratch` names a host-side stand-in, not a
+// device address: its address on each device is resolved once, with that
+// device current, by hipGetSymbolAddress, and only that pointer is passed to
+// kernels.  The counters are cleared when the address is resolved; each split
+// call's last workgroup returns its tile's counter to zero.
+constexpr size_t kScratchFloats = (size_t)1 << 20;
+constexpr int kScratchTiles = 1024;
+static __device__ __align__(256) float scratch[kScratchFloats + kScratchTiles];
+
+__global__ void fill_u32_kernel(unsigned* p, int n, unsigned v) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+struct ScratchDev {
+  SplitWs ws;
+  bool ready;
+};
+ScratchDev g_scr[kMaxDevices];
+
+// This device's scratch (resolved and cleared on stream s at the first call
+// per device), or nullptr with *err set.
+const SplitWs* scratch_ws(hipStream_t s, hipError_t* err) {
+  int dev = 0;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_ws_mu);
+  ScratchDev& d = g_scr[dev];
+  if (!d.ready) {
+    void* ptr = nullptr;
+    *err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (*err != hipSuccess || !ptr) return nullptr;
+    float* base = static_cast<float*>(ptr);
+    unsigned* cnt = reinterpret_cast<unsigned*>(base + kScratchFloats);
+    hipLaunchKernelGGL(fill_u32_kernel, dim3((kScratchTiles + 255) / 256), dim3(256), 0, s, cnt,
+                       kScratchTiles, 0u);
+    *err = hipGetLastError();
+    if (*err != hipSuccess) return nullptr;
+    d.ws.part = base;
+    d.ws.cnt = cnt;
+    d.ready = true;
+  }
+  return &d.ws;
+}
+
 // Number of K splits for a skinny grid of `tiles` workgroups.  Measured on
 // MI355X (bs=1 expert, prefix and connector shapes): a split costs ~1-2 us of
 // partial stores, counter round trip and partial loads, which only long K
@@ -1743,8 +1796,13 @@ int dispatch(const GemmArgs& p, int epi, int act, TileId t, dim3 grid, hipStream
   return 0;
 }
 
+// Where the split-K partials of skinny problems go: the allocated per-device
+// workspace (svla_linear_bf16 and the other entry points) or the static
+// scratch array (svla_linear_scratch_bf16).
+enum WsKind { WS_ALLOCATED = 0, WS_SCRATCH = 1 };
+
 template <int AMODE>
-int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
+int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s, WsKind wk = WS_ALLOCATED) {
   if (p.M < 0 || p.N <= 0 || p.K <= 0) return SVLA_EINVAL;
   if (p.M == 0) return 0;
   if (p.K % 8 || p.N % 4 || p.ldb % 8 || p.ldc % 4) return SVLA_EINVAL;
@@ -1771,7 +1829,18 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s) {
   }
   if (t.id == S32 || t.id == S64 || t.id == S16) {
     const int S = pick_split(gm * gn, p.K, t.bm, t.bn);
-    const SplitWs* w = S > 1 ? split_ws(s) : nullptr;
+    const SplitWs* w = nullptr;
+    if (S > 1 && wk == WS_SCRATCH) {
+      // the same split as the allocated workspace would take, or an error:
+      // the results stay bit-identical to svla_linear_bf16's
+      if ((size_t)gm * gn * S * (t.bm * t.bn + t.bm) > kScratchFloats || gm * gn > kScratchTiles)
+        return SVLA_ENOSPC;
+      hipError_t e = hipSuccess;
+      w = scratch_ws(s, &e);
+      if (!w) return e != hipSuccess ? (int)e : SVLA_EINVAL;
+    } else if (S > 1) {
+      w = split_ws(s);
+    }
     if (w) {
       p.ws = w->part;
       p.ws_cnt = w->cnt;
@@ -1844,6 +1913,32 @@ int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void*
   p.norm_w = static_cast<const bf16*>(norm_w);
   p.norm_eps = norm_eps;
   return run_gemm<A_DENSE>(p, EPI_STORE, act, (hipStream_t)stream);
+}
+
+int svla_linear_scratch_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
+                             const float* bias_f32, const void* res, int ldr, void* c, int ldc,
+                             int m, int n, int k, float alpha, int act, int out_f32,
+                             const void* norm_w, float norm_eps, svla_stream_t stream) {
+  if (act < 0 || act > SVLA_ACT_SILU) return SVLA_EINVAL;
+  if (out_f32 && (act || res)) return SVLA_EINVAL;
+  if (bias_f32 && !svla_aligned16(bias_f32)) return SVLA_EINVAL;
+  GemmArgs p = base_args(a, lda, w, ldw, c, ldc, m, n, k);
+  p.alpha = alpha;
+  p.bias = static_cast<const bf16*>(bias);
+  p.bias_f32 = bias_f32;
+  p.res = static_cast<const bf16*>(res);
+  p.ldr = ldr;
+  p.out_f32 = out_f32;
+  p.norm_w = static_cast<const bf16*>(norm_w);
+  p.norm_eps = norm_eps;
+  return run_gemm<A_DENSE>(p, EPI_STORE, act, (hipStream_t)stream, WS_SCRATCH);
+}
+
+int svla_init(void) {
+  if (!split_ws(nullptr)) return hipErrorOutOfMemory;
+  hipError_t e = hipSuccess;
+  if (!scratch_ws(nullptr, &e)) return e != hipSuccess ? (int)e : SVLA_EINVAL;
+  return (int)hipDeviceSynchronize();
 }
 
 int svla_linear_wide_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,

@@ -21,6 +21,7 @@ _fp = ctypes.POINTER(ctypes.c_float)
 # name -> argtypes (all return int)
 SIGNATURES = {
     "svla_version": [],
+    "svla_init": [],
     "svla_rmsnorm_bf16": [_p, _i, _p, _p, _i, _i, _i, _f, _p],
     "svla_layernorm_bf16": [_p, _i, _p, _p, _p, _i, _i, _i, _f, _p],
     "svla_layernorm_blocked_bf16": [_p, _i, _p, _p, _p, _i, _i, _f, _p],
@@ -31,6 +32,8 @@ SIGNATURES = {
     "svla_slab_block_bf16": [_p, _i, _p, _i, _i, _p],
     "svla_linear_bf16": [_p, _i, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _i, _i, _p, _f,
                          _p],
+    "svla_linear_scratch_bf16": [_p, _i, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _i, _i,
+                                 _p, _f, _p],
     "svla_linear_rope_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _f, _p],
     "svla_linear_silu_mul_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _p, _f, _p],
     "svla_patch_embed_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
@@ -89,6 +92,8 @@ class SvlaError(RuntimeError):
 def call(name: str, *args):
     rc = getattr(load(), name)(*args)
     if rc != 0:
-        what = "invalid argument (shape / alignment)" if rc == -22 else f"HIP error {rc}"
+        what = ("invalid argument (shape / alignment)" if rc == -22 else
+                "split needs more scratch than the static array holds" if rc == -28 else
+                f"HIP error {rc}")
         raise SvlaError(f"{name}: {what}")
     return rc

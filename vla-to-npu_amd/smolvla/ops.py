@@ -78,6 +78,15 @@ def layernorm(x, g, b, eps, out=None, blocked=False):
 
 
 # ------------------------------------------------------------------ GEMM ---
+def init(device=None):
+    """``svla_init`` on ``device`` (default: the current one): allocates the
+    split-K workspace up front, so eager calls and calls captured into a HIP
+    graph split long-K skinny GEMMs the same way; resolves the static scratch
+    of :func:`linear_scratch`.  Once per device, before any capture."""
+    with torch.cuda.device(device if device is not None else torch.cuda.current_device()):
+        _lib.call("svla_init")
+
+
 def linear(a, w, bias=None, bias_f32=None, res=None, act=None, alpha=1.0, out=None,
            out_f32=False, norm=None):
     """``epilogue(alpha * norm(a) @ w.T)``; ``w`` packed ``[N, K]``;

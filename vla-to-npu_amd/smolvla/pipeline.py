@@ -39,6 +39,7 @@ class SmolVLAEngine:
         self.use_graph = use_graph
         self.graph = None
         with torch.cuda.device(self.device):
+            ops.init()
             self._prepare(params)
             self._alloc()
 
