@@ -255,6 +255,97 @@ int svla_action_out_euler(const void* a, int lda, const void* w, int ldw, float*
                           int ldx, void* x_bf16, int ldxb, int m, int n, int k,
                           const void* norm_w, float norm_eps, float dt, svla_stream_t stream);
 
+/* ------------------------------------------------------- fused expert --
+ * The whole flow-matching action expert of one chunk -- num_steps Euler steps,
+ * each: action_in (Linear A->H + bias), time_in on [action | time] (the time
+ * half precomputed per step into time_bias) + SiLU, time_out (+ bias), the
+ * n_layers expert layers (self-attention, causal, when layer % 2 == 0, else
+ * cross-attention on the projected prefix K/V; RMSNorm -> QKV (+RoPE) ->
+ * attention -> O + residual -> RMSNorm -> gate|up + SiLU*up -> down +
+ * residual), the final RMSNorm + action_out and x <- x + dt * v -- in ONE
+ * persistent launch for small batches (batch * chunk rows; chunk <= 64).
+ * Same arithmetic and rounding points as the layer-by-layer entry points
+ * (svla_linear_*_bf16, svla_attention_bf16, svla_action_out_euler), except
+ * that the attention softmax is normalised before its probabilities are
+ * rounded to bf16, as the reference torch module does.  Replaces
+ * action_expert_self_forward / action_expert_cross_forward
+ * (vla/action_expert_bf16.py:662-803) as driven by joint_transformer
+ * (vla/vla.py:194-212) and postprocessing (vla/vla.py:218-222), plus the
+ * Euler loop, time embedding and action input the reference lacks.
+ * Weights are PACKED [out, in] as for svla_linear_bf16; w_gu interleaved by
+ * svla_pack_gate_up_bf16; self layers' w_qkv is [q | k | v, hidden], cross
+ * layers' w_qkv is Wq [q, hidden] and cross_k / cross_v are the already
+ * projected prefix K/V [batch * prefix_len, kv] (leading dimension ld_cross).
+ * rope_cos/sin [chunk, 32] (svla_rope_table).  x_in / x_out: fp32
+ * [batch * chunk, action_dim] Euler state before / after (may alias). */
+typedef struct svla_expert_layer {
+  int cross;
+  const void* w_qkv;
+  const void* w_o;
+  const void* w_gu;
+  const void* w_down;
+  const void* norm1;
+  const void* norm2;
+  const void* cross_k;
+  const void* cross_v;
+} svla_expert_layer;
+
+typedef struct svla_expert_desc {
+  int batch, chunk, hidden, n_q_heads, n_kv_heads, head_dim, inter, action_dim, n_layers,
+      prefix_len, num_steps, ld_cross;
+  float rms_eps, dt;
+  const void* w_action_in; /* [hidden, action_dim] */
+  const void* b_action_in; /* [hidden] */
+  const void* w_time_in_a; /* [hidden, hidden]: the action half of time_in */
+  const float* time_bias;  /* [num_steps, hidden] fp32: temb(t_s) . W_time_in[time half] + b */
+  const void* w_time_out;  /* [hidden, hidden] */
+  const void* b_time_out;  /* [hidden] */
+  const void* norm_out;    /* [hidden] final RMSNorm gain */
+  const void* w_action_out; /* [action_dim, hidden] */
+  const float* rope_cos;
+  const float* rope_sin;
+  const float* x_in;
+  float* x_out;
+  const svla_expert_layer* layers; /* host array of n_layers */
+} svla_expert_desc;
+
+/* What svla_expert_run needs (filled by svla_expert_prepare; host memory). */
+typedef struct svla_expert_plan {
+  void* phases;
+  int n_phases;
+  unsigned* counters;
+  long counter_words;
+  unsigned* status;
+  int grid;
+  int team_xcd;
+  int team_size;
+} svla_expert_plan;
+
+/* Device workspace bytes svla_expert_prepare needs for d (phase table,
+ * arrival counters, and one buffer per intermediate activation of the whole
+ * chunk: about 9.4 MB per Euler step at batch 1), or 0 if d is invalid
+ * (chunk > 64, head_dim != 64, hidden / inter / q width > 2048, prefix_len >
+ * 256, a NULL pointer). */
+long svla_expert_workspace_size(const svla_expert_desc* d);
+
+/* Lays out the workspace (device, 256-byte aligned, ws_bytes >= the size
+ * above), uploads the phase table (synchronous on `stream`) and fills
+ * *plan.  team_xcd < 0: every CU takes part; 0..7: only the CUs of that XCD
+ * (a performance choice: results are the same).  The pointers in d are
+ * captured: later runs use them. */
+int svla_expert_prepare(const svla_expert_desc* d, void* ws, long ws_bytes, int team_xcd,
+                        svla_expert_plan* plan, svla_stream_t stream);
+
+/* One chunk's expert: clears the arrival counters (a small kernel) and
+ * launches the persistent kernel (one workgroup per CU) on `stream`;
+ * graph-capturable.  Every wait inside is bounded: a launch that cannot
+ * finish (workgroups not co-resident) gives up and sets the status word. */
+int svla_expert_run(const svla_expert_plan* plan, svla_stream_t stream);
+
+/* Status word of the last run (synchronous copy): 0 ok, 1 a wait gave up,
+ * 2 the XCD team could not form. */
+int svla_expert_status(const svla_expert_plan* plan, int* status);
+
 /* ------------------------------------------------------------ attention --
  * Fused GQA attention: O = softmax(scale * Q K^T + mask) V per head, query
  * head h reading KV head h*hkv/hq.  Scores and softmax statistics fp32,

@@ -637,3 +637,41 @@ def test_bad_shapes_raise(ops):
     q = torch.zeros(1, 4, 96, dtype=BF16, device="cuda")         # head_dim != 64 layout
     with pytest.raises(SvlaError):
         ops.attention(q, q, q, q, 2, 1)
+
+
+@pytest.mark.parametrize("kind", ["silu_mul", "rope", "attention"])
+def test_lds_pipeline_repeat_is_bit_stable(ops, kind):
+    """Regression: the LDS-DMA pipelines (64x64 GEMM tile with fused RMSNorm,
+    used by the batch-1 prefix's norm + gate|up and norm + QKV + RoPE, and
+    the attention kernel) once refilled an LDS stage before every wave had
+    finished reading it, so one wave's 16 rows of a tile occasionally read
+    the next K tile's data (4 of 12 prefix passes differed).  The same launch,
+    repeated with other work between, must give the same bits every time."""
+    g = gen(77)
+    M, K = 241, 960
+    x = torch.randn(M, K, generator=g).to(BF16).cuda()
+    gain = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16).cuda()
+    if kind == "silu_mul":
+        wg = (0.02 * torch.randn(K, 2560, generator=g)).to(BF16).cuda()
+        wu = (0.02 * torch.randn(K, 2560, generator=g)).to(BF16).cuda()
+        w = ops.pack_gate_up(wg, wu)
+        out = torch.empty(M, 2560, dtype=BF16, device="cuda")
+        run = lambda: ops.linear_silu_mul(x, w, out=out, norm=(gain, 1e-5))  # noqa: E731
+    elif kind == "rope":
+        w = ops.pack_weight((0.02 * torch.randn(K, 1600, generator=g)).to(BF16).cuda())
+        cos, sin = ops.rope_table(M, 64, 1e5, device="cuda")
+        out = torch.empty(M, 1600, dtype=BF16, device="cuda")
+        run = lambda: ops.linear_rope(x, w, 1280, M, cos, sin, out=out, norm=(gain, 1e-5))  # noqa: E731
+    else:
+        qkv = torch.randn(M, 1600, generator=g).to(BF16).cuda().view(1, M, 1600)
+        out = torch.empty(1, M, 960, dtype=BF16, device="cuda")
+        run = lambda: ops.attention(qkv[:, :, :960], qkv[:, :, 960:1280], qkv[:, :, 1280:],  # noqa: E731
+                                    out, 15, 5, "prefix_lm", 240)
+    run()
+    first = out.clone()
+    noise = torch.randn(1 << 22, device="cuda")
+    for i in range(40):
+        if i % 4 == 0:
+            noise.mul_(1.0001).sum().item()          # other work between launches
+        run()
+        assert torch.equal(out, first), f"{kind}: launch {i} differs"

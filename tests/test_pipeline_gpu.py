@@ -155,3 +155,22 @@ def test_batch32_engine_matches_oracle_and_batch1():
         worst = max(worst, (r - got[b:b + 1]).abs().max().item())
     print(f"batch 32 vs batch-1 engine, all rows: max abs {worst:.3e}")
     assert worst <= ACTION_ATOL
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_batch1_replays_bit_stable(full, fused):
+    """The batch-1 engine (the latency path: skinny and 64x64 LDS-DMA GEMMs,
+    the fused or layer-by-layer expert) gives the same bits on every graph
+    replay and in eager mode."""
+    from smolvla.pipeline import SmolVLAEngine
+    cfg, P, inputs, want, _ = full
+    dev = [t[:1].cuda() for t in inputs]
+    eng = SmolVLAEngine(cfg, P, batch=1, fused_expert=fused)
+    first = eng.run(*dev).clone()
+    for i in range(4):
+        torch.randn(1 << 20, device="cuda").sum().item()
+        assert torch.equal(eng.run(*dev), first), f"replay {i} differs"
+    eager = SmolVLAEngine(cfg, P, batch=1, use_graph=False, fused_expert=fused)
+    for i in range(2):
+        assert torch.equal(eager.run(*dev), first), f"eager run {i} differs"
+    assert (first.cpu() - want[:1]).abs().max().item() <= ACTION_ATOL

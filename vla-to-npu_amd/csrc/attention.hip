@@ -271,9 +271,19 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
     }
   };
 
-  // s_waitcnt vmcnt(N): a stage is 4 DMA instructions per wave; the next
-  // stage stays in flight (gfx9 encoding, expcnt / lgkmcnt unconstrained)
-  constexpr int kWaitOne = 0xF70 | 4;
+  // Before each barrier: s_waitcnt vmcnt(4) lgkmcnt(0).  vmcnt: a stage is 4
+  // DMA instructions per wave and the next stage stays in flight.
+  // lgkmcnt(0): this wave's LDS reads of the stage computed before the
+  // barrier have completed, since the DMA issued right after the barrier
+  // refills that stage (the compiler would otherwise wait only at the reads'
+  // first use, after the refill's issue).  gfx9 encoding, expcnt unconstrained.
+  constexpr int kWaitOne = 0x070 | 4;
+  auto sync_step = [&]() __attribute__((always_inline)) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(kWaitOne);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
@@ -288,18 +298,15 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
   // barrier rounds.  (The same exits in the FULL kernel measured 6-7% slower
   // on the ViT's 16-block loop, so that loop keeps its original form.)
   for (int blk = 0; blk < nb; blk += 3) {
-    __builtin_amdgcn_s_waitcnt(kWaitOne);
-    __builtin_amdgcn_s_barrier();
+    sync_step();
     issue(I2{}, blk + 2);
     compute(I0{}, blk);
     if (!FULL && blk + 1 >= nb) break;
-    __builtin_amdgcn_s_waitcnt(kWaitOne);
-    __builtin_amdgcn_s_barrier();
+    sync_step();
     issue(I0{}, blk + 3);
     if (blk + 1 < nb) compute(I1{}, blk + 1);
     if (!FULL && blk + 2 >= nb) break;
-    __builtin_amdgcn_s_waitcnt(kWaitOne);
-    __builtin_amdgcn_s_barrier();
+    sync_step();
     issue(I1{}, blk + 4);
     if (blk + 2 < nb) compute(I2{}, blk + 2);
   }

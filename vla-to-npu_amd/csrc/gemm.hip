@@ -665,13 +665,26 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
     mma(fw, fx);
   };
 
-  // s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained: each stage
-  // is A_DMA + B_DMA instructions per wave and two newer stages may stay in
-  // flight (gfx9 encoding: vmcnt[3:0] in bits 3:0, expcnt = 7 in bits 6:4,
-  // lgkmcnt = 15 in bits 11:8)
+  // Before each barrier: s_waitcnt vmcnt(N) lgkmcnt(0).  vmcnt: each stage is
+  // A_DMA + B_DMA instructions per wave and two newer stages may stay in
+  // flight, so the stage computed next has landed.  lgkmcnt(0): this wave's
+  // LDS reads of the stage computed before the barrier have completed, since
+  // the DMA issued right after the barrier refills that stage.  (Without it
+  // the compiler defers the wait to the reads' first use, after the barrier
+  // and the refill's issue; a refill that hits in L2 could then overwrite a
+  // fragment before a busy LDS served the read: one wave's 16 rows of a tile
+  // read the wrong K tile, rarely and timing-dependent, measured on MI355X.)
+  // gfx9 encoding: vmcnt[3:0] in bits 3:0, expcnt = 7 in bits 6:4, lgkmcnt
+  // in bits 11:8.
   constexpr int kWaitN = 2 * (A_DMA + B_DMA);
   static_assert(kWaitN <= 15, "vmcnt immediate");
-  constexpr int kWait2 = 0xF70 | kWaitN;
+  constexpr int kWait2 = 0x070 | kWaitN;
+  auto sync_step = [&]() __attribute__((always_inline)) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(kWait2);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
@@ -681,20 +694,16 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
   issue(I1{}, 1);
   issue(I2{}, 2);
   for (int kt = 0; kt < nk; kt += 4) {
-    __builtin_amdgcn_s_waitcnt(kWait2);
-    __builtin_amdgcn_s_barrier();
+    sync_step();
     issue(I3{}, kt + 3);
     compute(I0{}, kt);
-    __builtin_amdgcn_s_waitcnt(kWait2);
-    __builtin_amdgcn_s_barrier();
+    sync_step();
     issue(I0{}, kt + 4);
     if (kt + 1 < nk) compute(I1{}, kt + 1);
-    __builtin_amdgcn_s_waitcnt(kWait2);
-    __builtin_amdgcn_s_barrier();
+    sync_step();
     issue(I1{}, kt + 5);
     if (kt + 2 < nk) compute(I2{}, kt + 2);
-    __builtin_amdgcn_s_waitcnt(kWait2);
-    __builtin_amdgcn_s_barrier();
+    sync_step();
     issue(I2{}, kt + 6);
     if (kt + 3 < nk) compute(I3{}, kt + 3);
   }

@@ -18,7 +18,32 @@ _f = ctypes.c_float
 _d = ctypes.c_double
 _fp = ctypes.POINTER(ctypes.c_float)
 
-# name -> argtypes (all return int)
+class ExpertLayer(ctypes.Structure):
+    """``svla_expert_layer`` (include/svla.h)."""
+    _fields_ = [("cross", ctypes.c_int), ("w_qkv", _p), ("w_o", _p), ("w_gu", _p),
+                ("w_down", _p), ("norm1", _p), ("norm2", _p), ("cross_k", _p), ("cross_v", _p)]
+
+
+class ExpertDesc(ctypes.Structure):
+    """``svla_expert_desc`` (include/svla.h)."""
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "batch", "chunk", "hidden", "n_q_heads", "n_kv_heads", "head_dim", "inter",
+        "action_dim", "n_layers", "prefix_len", "num_steps", "ld_cross")] + [
+        ("rms_eps", ctypes.c_float), ("dt", ctypes.c_float),
+        ("w_action_in", _p), ("b_action_in", _p), ("w_time_in_a", _p), ("time_bias", _p),
+        ("w_time_out", _p), ("b_time_out", _p), ("norm_out", _p), ("w_action_out", _p),
+        ("rope_cos", _p), ("rope_sin", _p), ("x_in", _p), ("x_out", _p),
+        ("layers", ctypes.POINTER(ExpertLayer))]
+
+
+class ExpertPlan(ctypes.Structure):
+    """``svla_expert_plan`` (include/svla.h)."""
+    _fields_ = [("phases", _p), ("n_phases", ctypes.c_int), ("counters", _p),
+                ("counter_words", ctypes.c_long), ("status", _p), ("grid", ctypes.c_int),
+                ("team_xcd", ctypes.c_int), ("team_size", ctypes.c_int)]
+
+
+# name -> argtypes (all return int, except RESTYPES)
 SIGNATURES = {
     "svla_version": [],
     "svla_init": [],
@@ -60,9 +85,14 @@ SIGNATURES = {
     "svla_row_norm": [_p, _i, _p, _p, _p, _i, _i, _i, _f, _i, _i, _i, _p],
     "svla_softmax_rows": [_p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _p],
     "svla_conv_patch_f32": [_p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
+    "svla_expert_workspace_size": [ctypes.POINTER(ExpertDesc)],
+    "svla_expert_prepare": [ctypes.POINTER(ExpertDesc), _p, _l, _i, ctypes.POINTER(ExpertPlan),
+                            _p],
+    "svla_expert_run": [ctypes.POINTER(ExpertPlan), _p],
+    "svla_expert_status": [ctypes.POINTER(ExpertPlan), ctypes.POINTER(ctypes.c_int)],
 }
 
-RESTYPES = {}
+RESTYPES = {"svla_expert_workspace_size": ctypes.c_long}
 
 _LIB = None
 

@@ -36,6 +36,13 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
+def _addr(t):
+    """Device address of a GPU tensor as an int (for ctypes struct fields)."""
+    if not t.is_cuda:
+        raise ValueError("smolvla ops take GPU tensors (no CPU fallback)")
+    return t.data_ptr()
+
+
 def _ld(t):
     if t.dim() != 2 or t.stride(-1) != 1:
         raise ValueError(f"expected a row-major 2-D view, got shape {tuple(t.shape)} "
@@ -78,6 +85,63 @@ def layernorm(x, g, b, eps, out=None, blocked=False):
 
 
 # ------------------------------------------------------------------ GEMM ---
+class FusedExpert:
+    """The whole flow-matching action expert of one chunk in one persistent
+    launch (``svla_expert_*``): prepared once for fixed buffers (weights,
+    projected cross K/V, Euler state), then :meth:`run` per chunk on the
+    current stream (graph-capturable)."""
+
+    def __init__(self, cfg, expert_layers, cross, io, rope, tbias, x_state, batch, dt,
+                 team_xcd=-1):
+        e = cfg.expert
+        self._keep = []                       # tensors the device table points at
+        layers = (_lib.ExpertLayer * cfg.expert_layers)()
+        for i, P in enumerate(expert_layers):
+            L = layers[i]
+            L.cross = int(cfg.is_cross(i))
+            L.w_qkv = _addr(P["wq"] if L.cross else P["wqkv"])
+            L.w_o, L.w_gu, L.w_down = _addr(P["wo"]), _addr(P["wgu"]), _addr(P["wd"])
+            L.norm1, L.norm2 = _addr(P["n1"]), _addr(P["n2"])
+            if L.cross:
+                ck, cv = cross[i]
+                if ck.stride(0) != cv.stride(0):
+                    raise ValueError("cross K and V need one leading dimension")
+                L.cross_k, L.cross_v = _addr(ck), _addr(cv)
+                ld_cross = ck.stride(0)
+        d = _lib.ExpertDesc()
+        d.batch, d.chunk, d.hidden = batch, cfg.chunk, e.hidden
+        d.n_q_heads, d.n_kv_heads, d.head_dim, d.inter = e.n_q_heads, e.n_kv_heads, e.head_dim, e.inter
+        d.action_dim, d.n_layers, d.prefix_len = cfg.action_dim, cfg.expert_layers, cfg.prefix_len
+        d.num_steps, d.ld_cross = cfg.num_steps, ld_cross
+        from .config import resolve_eps
+        d.rms_eps, d.dt = resolve_eps(e.rms_eps), float(dt)
+        d.w_action_in, d.b_action_in = _addr(io["w_ain"]), _addr(io["b_ain"])
+        d.w_time_in_a, d.time_bias = _addr(io["w_tin_a"]), _addr(tbias)
+        d.w_time_out, d.b_time_out = _addr(io["w_tout"]), _addr(io["b_tout"])
+        d.norm_out, d.w_action_out = _addr(io["n_exp"]), _addr(io["w_aout"])
+        d.rope_cos, d.rope_sin = _addr(rope.cos), _addr(rope.sin)
+        d.x_in = d.x_out = _addr(x_state)
+        d.layers = layers
+        lib = _lib.load()
+        nbytes = lib.svla_expert_workspace_size(ctypes.byref(d))
+        if nbytes <= 0:
+            raise ValueError("fused expert: configuration not supported")
+        self.workspace = torch.empty(nbytes + 256, dtype=torch.uint8, device=x_state.device)
+        base = (self.workspace.data_ptr() + 255) // 256 * 256
+        self.plan = _lib.ExpertPlan()
+        _lib.call("svla_expert_prepare", ctypes.byref(d), ctypes.c_void_p(base), nbytes,
+                  int(team_xcd), ctypes.byref(self.plan), _stream())
+        self.desc, self.layers = d, layers
+
+    def run(self):
+        _lib.call("svla_expert_run", ctypes.byref(self.plan), _stream())
+
+    def status(self):
+        st = ctypes.c_int(-1)
+        _lib.call("svla_expert_status", ctypes.byref(self.plan), ctypes.byref(st))
+        return st.value
+
+
 def init(device=None):
     """``svla_init`` on ``device`` (default: the current one): allocates the
     split-K workspace up front, so eager calls and calls captured into a HIP

@@ -31,13 +31,29 @@ BF16 = torch.bfloat16
 F32 = torch.float32
 
 
+# the fused (one persistent launch) expert is used up to this many rows
+# (batch * chunk): one 64-row block per GEMM unit
+FUSED_EXPERT_MAX_ROWS = 64
+
+
 class SmolVLAEngine:
-    def __init__(self, cfg: SmolVLAConfig, params, batch: int, device="cuda", use_graph=True):
+    """``fused_expert``: run the 10-step action expert as one persistent
+    launch (``ops.FusedExpert``) instead of ~840 layer-by-layer launches;
+    default: when batch * chunk <= FUSED_EXPERT_MAX_ROWS (batch 1).
+    ``expert_team_xcd``: the fused expert's CUs (-1: all; 0..7: one XCD)."""
+
+    def __init__(self, cfg: SmolVLAConfig, params, batch: int, device="cuda", use_graph=True,
+                 fused_expert=None, expert_team_xcd=-1):
         self.cfg = cfg
         self.B = batch
         self.device = torch.device(device)
         self.use_graph = use_graph
         self.graph = None
+        if fused_expert is None:
+            fused_expert = batch * cfg.chunk <= FUSED_EXPERT_MAX_ROWS
+        self.fused_expert = fused_expert
+        self.expert_team_xcd = expert_team_xcd
+        self.fx = None
         with torch.cuda.device(self.device):
             ops.init()
             self._prepare(params)
@@ -110,6 +126,13 @@ class SmolVLAEngine:
         # weights and the fixed Euler schedule: computed once, like the RoPE
         # tables, not per chunk
         self.time_bias(self.schedule())
+        if self.fused_expert:
+            io = dict(w_ain=self.w_ain, b_ain=self.b_ain, w_tin_a=self.w_tin_a,
+                      w_tout=self.w_tout, b_tout=self.b_tout, n_exp=self.n_exp,
+                      w_aout=self.w_aout)
+            self.fx = ops.FusedExpert(cfg, self.expert, self.cross, io, self.rope_expert,
+                                      self.tbias, self.x_t, B, -1.0 / cfg.num_steps,
+                                      team_xcd=self.expert_team_xcd)
         # materialise every lazily-named buffer before any capture
         self._forward()
         torch.cuda.synchronize(dev)
@@ -201,6 +224,9 @@ class SmolVLAEngine:
         self.run_prefix()
         self.project_cross()
         self.x_t.copy_(self.in_noise.view(-1, cfg.action_dim))
+        if self.fx is not None:
+            self.fx.run()
+            return
         ops.f32_to_bf16(self.x_t, out=self.x_bf)
         dt = -1.0 / cfg.num_steps
         for s in range(cfg.num_steps):
