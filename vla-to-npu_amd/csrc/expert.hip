@@ -11,19 +11,20 @@
 // small corner of the chip; here the work is a fixed list of PHASES (one per
 // GEMM or attention of the step sequence) that every workgroup walks.
 //
-// Design (CDNA4, measured on MI355X with a microbenchmark of this build):
+// Design (CDNA4; the figures are MI355X measurements of this build):
 //  * One workgroup of 8 waves per CU.  A phase is split into UNITS (a
-//    64-row x 16-column output tile of a GEMM, or one (sample, head) of an
+//    64-row x 16-column output tile of a GEMM, one (sample, head) of an
 //    attention); unit u of a phase runs on team rank u % team_size.
 //  * Phases hand over through device-scope arrival counters: a workgroup
 //    that finished its units of phase p waits for its stores to be
 //    acknowledged (vmcnt = 0), then adds its unit count to one of 8
-//    sub-counters of phase p (spread so that 256 arrivals do not queue on one
-//    address: a grid barrier measured 4.0 us with one counter, 2.0 us with
-//    8); a workgroup with units in phase p + 1 polls the 8 sub-counters (8
-//    lanes, agent-scope atomic loads) until they sum to phase p's unit count.
-//    Completion of phase p implies completion of every earlier phase (each of
-//    its units waited for p - 1), so one wait per phase suffices.
+//    sub-counters of phase p (spread so that 256 arrivals do not queue on
+//    one address: a grid barrier measured 4.0 us with one counter, 2.0 us
+//    with 8); a workgroup with units in phase p + 1 polls the 8
+//    sub-counters (with the status word, one round trip per poll) until they
+//    sum to phase p's unit count.  Completion of phase p implies completion
+//    of every earlier phase (each of its units waited for p - 1), so one
+//    wait per phase suffices.
 //  * Every phase writes its output to a buffer that no other phase of the
 //    launch writes (activation versions, not in-place updates), 256-byte
 //    aligned, with write-through (agent-scope) stores.  No cache can then
@@ -31,21 +32,31 @@
 //    the phase that writes it has completed, so the first read of a line by
 //    an XCD misses its L2 and later reads by that XCD's CUs hit the fresh
 //    line.  Activations are read with plain loads (L2-cached broadcast).
-//  * Weights never depend on the previous phase: a workgroup issues the
-//    weight loads of its first unit of a phase BEFORE it waits for the
-//    phase's inputs (register prefetch), so the weight latency overlaps the
-//    hand-off; further units of the same phase prefetch during the epilogue.
-//  * GEMM units are the skinny kernel's: 8 waves split K, each wave holds its
-//    k-range of the 64 activation rows in registers for the whole phase and
-//    one 16x16x32 MFMA fragment of weights per k-step; the 8 partial tiles
-//    meet in LDS.  The RMSNorm in front of a projection is fused (gain on the
-//    way into the MFMAs, row sums of squares from the same fragments, 1/rms
-//    in the epilogue).  Paired epilogues (RoPE pairs (d, d+32), SiLU(gate) *
-//    up) use the 16-column tile of 8 columns + their partners.
-//  * Attention units: one (sample, head) on 4 waves of 16 queries each; V is
-//    staged transposed in LDS, scores are fp32, the softmax is computed
-//    exactly (max, sum, divide) and the probabilities rounded to bf16 before
-//    P.V, as the reference torch module does (vla/text_encoder_bf16.py:117-126).
+//  * Latency, not bandwidth, sets the time of a phase at these sizes
+//    (per-phase timestamps: ~1.2 us hand-off, ~2-3 us for the activation
+//    loads, the rest epilogue and bookkeeping), so everything that does not
+//    depend on the previous phase is issued before or beside its wait: the
+//    weights of a workgroup's first unit before the wait, the epilogue
+//    operands (residual, bias, RoPE tables, Euler state) together with the
+//    activations, the next phase's header during the current phase.
+//  * GEMM units: the 8 waves split K (one pass for K <= 2048); each wave
+//    holds its k-range of the 64 activation rows in registers and streams
+//    its 16x16x32 MFMA weight fragments into a private LDS region by LDS-DMA
+//    (no registers held while they fly); the partial tiles meet in LDS.
+//    The RMSNorm in front of a projection is fused (gain on the way into the
+//    MFMAs, row sums of squares from the same fragments, 1/rms in the
+//    epilogue).  Paired epilogues (RoPE pairs (d, d+32), SiLU(gate) * up) use
+//    the 16-column tile of 8 columns + their partners.  The V columns of a
+//    self layer's QKV projection are written transposed (V^T [kv][64 keys])
+//    for the attention.
+//  * Attention units: one (sample, head); K, V^T and the queries are staged
+//    into LDS once per CU (cross layers: K and V^T before the phase wait),
+//    then the 8 waves take 4 key quarters of 64 keys x 2 query groups.  Scores are fp32; the softmax is exact (the
+//    maxima and sums of the key groups meet in LDS) and the probabilities
+//    are rounded to bf16 before P.V, as the reference torch module does
+//    (vla/text_encoder_bf16.py:117-126).  The P.V operand is V^T straight
+//    from global memory (the cross layers' V is transposed by the launch's
+//    first phase).
 //  * Every wait is bounded: past kSpin polls (or when another workgroup has
 //    already given up) the workgroup sets the status word and leaves, so the
 //    grid always drains.  The team is either every workgroup of the launch
@@ -53,7 +64,6 @@
 //    XCC_ID register); the write-through / write-once discipline keeps the
 //    results correct whichever CUs take part.
 #include <cstring>
-#include <mutex>
 #include <vector>
 
 #include "svla_common.h"
@@ -62,25 +72,28 @@ namespace {
 
 constexpr int XW = 8;              // waves per workgroup
 constexpr int XT = XW * 64;        // threads per workgroup
-constexpr int XKS = 4;             // 32-deep k-steps per wave and pass
-constexpr int XPASS = 2;           // passes per unit: K <= XW * XKS * 32 * XPASS = 2048
-constexpr int XBM = 64;            // rows per GEMM unit (4 MFMA row tiles)
+constexpr int XKS = 64 / XW;       // 32-deep k-steps per wave: K <= XW * XKS * 32 = 2048
+constexpr int XBM = 64;            // rows per GEMM unit (4 MFMA row tiles) = max batch * chunk
 constexpr int XBN = 16;            // columns per GEMM unit
 constexpr int XPS = XBN + 4;       // padded LDS row of a partial tile (floats)
-constexpr int XMAXQ = 64;          // attention: queries per sample
 constexpr int XMAXK = 256;         // attention: keys per sample
-constexpr int XVT = XMAXK + 8;     // padded LDS row of V^T (bf16)
+constexpr int XKQ = 4;             // attention: key quarters (waves = XW / 4 query groups x 4)
+constexpr int XKW = XMAXK / XKQ;   // attention: keys per wave (64)
+constexpr int XQT = 4 / (XW / XKQ);  // attention: 16-query tiles per wave
+constexpr int XVTS = 64;           // self-attention V^T: keys per sample (leading dimension)
+constexpr int kMaxCross = 16;      // cross layers (V^T transposes in the first phase)
 constexpr int kSub = 8;            // sub-counters per phase
 constexpr int kCntStride = 32;     // unsigned per sub-counter (128 bytes apart)
 constexpr int kSpin = 1 << 22;     // polls before a wait gives up
 
-enum XKind { XK_GEMM = 0, XK_ATTN = 1 };
+enum XKind { XK_GEMM = 0, XK_ATTN = 1, XK_VT = 2 };
 enum XEpi { XE_STORE = 0, XE_ROPE = 1, XE_SILU = 2, XE_EULER = 3 };
 enum XStat { XS_OK = 0, XS_TIMEOUT = 1, XS_TEAM = 2 };
 
 struct XPhase {
   int kind, epi, act, a_f32;
   int M, N, K, units, col_tiles;
+  int row_groups, group_tiles;  // GEMM unit = (column tile, group of row tiles)
   // GEMM: C[M, N] = epilogue(norm(A)[M, K] . W[N, K]^T)
   const void* a;
   int lda;
@@ -97,22 +110,35 @@ struct XPhase {
   const float* cos_t;
   const float* sin_t;
   int rope_cols, rope_period;
+  bf16* vt;     // ROPE: columns >= rope_cols go here transposed, [sample][col][XVTS]
+  int chunk;    // rows per sample (ROPE V^T, attention queries)
   const float* x_in;  // Euler: x_out[m, n] = x_in[m, n] + dt * bf16(v) (fp32, leading dim N)
   float* x_out;
   float dt;
-  // attention: unit = sample * heads + head
+  // attention: unit = sample * heads + head; V given transposed
   const bf16* q;
   const bf16* k;
-  const bf16* v;
+  const bf16* vt_in;
   bf16* o;
-  int ldq, ldk, ldv, ldo;
-  long q_bs, k_bs, v_bs, o_bs;
-  int heads, kv_heads, lq, lk, causal;
+  int ldq, ldk, ldvt, ldo;
+  long q_bs, k_bs, vt_bs, o_bs;
+  int heads, kv_heads, lk, causal;
+  int kv_static;  // K and V^T were written before the previous phase (cross layers)
   float scale;
+  // V^T transposes (first phase): unit = (layer, sample, 64-column block)
+  int n_vt, vt_blocks, vt_ldv, vt_keys;
+  long vt_src_bs, vt_dst_bs;
+  const bf16* vt_src[kMaxCross];
+  bf16* vt_dst[kMaxCross];
 };
 
+// The phase table does not change while the kernel runs: reading it through
+// the constant address space lets uniform field reads become scalar loads
+// (cached in the scalar cache) instead of one vector round trip each.
+typedef const __attribute__((address_space(4))) XPhase CPhase;
+
 struct XArgs {
-  const XPhase* ph;
+  CPhase* ph;
   int n_ph;
   unsigned* cnt;     // [n_ph + 1][kSub][kCntStride]; the last row is the team registration
   unsigned* status;  // XStat of the launch (0 = ok)
@@ -125,9 +151,13 @@ struct XArgs {
 typedef const __attribute__((address_space(1))) bf16x8* gbf8p;
 typedef const __attribute__((address_space(1))) f32x4* gf4p;
 typedef const __attribute__((address_space(1))) bf16x4* gbf4p;
+typedef const __attribute__((address_space(1))) uint64_t* gu64cp;
+typedef const __attribute__((address_space(1))) uint16_t* gu16cp;
 __device__ __forceinline__ bf16x8 ldg8(const bf16* p) { return *(gbf8p)(p); }
 __device__ __forceinline__ bf16x4 ldg4(const bf16* p) { return *(gbf4p)(p); }
 __device__ __forceinline__ f32x4 ldgf4(const float* p) { return *(gf4p)(p); }
+__device__ __forceinline__ uint64_t ldg64(const bf16* p) { return *(gu64cp)(p); }
+__device__ __forceinline__ uint16_t ldg16(const bf16* p) { return *(gu16cp)(p); }
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 __device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
@@ -139,8 +169,8 @@ __device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
 constexpr int wc_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 constexpr int wc_lgkm0 = 15 | (3 << 14) | (7 << 4);
 
-// LDS written by this wave visible to the whole workgroup (global memory
-// operations in flight are not waited for)
+// LDS written by this wave visible to the whole workgroup, this wave's LDS
+// reads complete (global memory operations in flight are not waited for)
 __device__ __forceinline__ void wg_sync_lds() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(wc_lgkm0);
@@ -153,29 +183,31 @@ typedef __attribute__((address_space(1))) uint64_t* gu64p;
 __device__ __forceinline__ void st8_wt(void* p, uint64_t v) {
   __hip_atomic_store((gu64p)(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// 4 bf16 (8 bytes) stored write-through
-__device__ __forceinline__ void st4_wt(bf16* p, const float v[4]) {
+__device__ __forceinline__ uint64_t pack4(const float v[4]) {
   bf16x4 o;
   o[0] = f2bf(v[0]); o[1] = f2bf(v[1]); o[2] = f2bf(v[2]); o[3] = f2bf(v[3]);
-  st8_wt(p, __builtin_bit_cast(uint64_t, o));
+  return __builtin_bit_cast(uint64_t, o);
 }
+__device__ __forceinline__ void st4_wt(bf16* p, const float v[4]) { st8_wt(p, pack4(v)); }
 __device__ __forceinline__ void st2f_wt(float* p, float a, float b) {
   st8_wt(p, __builtin_bit_cast(uint64_t, u32x2{__builtin_bit_cast(uint32_t, a),
                                                __builtin_bit_cast(uint32_t, b)}));
 }
 
-// Thread 0 of wave 0's lanes 0..7 poll the 8 sub-counters of `row` until they
-// sum to `target`; false when the wait gave up (status set).  Wave 0 only.
+// Wave 0 polls the 8 sub-counters of `row` (lanes 0..7) and the status word
+// (lane 8) together until the counters sum to `target`; false when the wait
+// gave up (status set).
 __device__ bool wait_phase(const XArgs& g, int row, unsigned target) {
   const int lane = threadIdx.x & 63;
-  const unsigned* c = g.cnt + ((size_t)row * kSub + (lane & (kSub - 1))) * kCntStride;
+  const unsigned* c = lane < kSub ? g.cnt + ((size_t)row * kSub + lane) * kCntStride : g.status;
   for (int n = 0;; ++n) {
-    unsigned s = lane < kSub ? ld_agent(c) : 0u;
+    const unsigned v = lane <= kSub ? ld_agent(c) : 0u;
+    unsigned s = lane < kSub ? v : 0u;
     s += __shfl_xor(s, 1, 64);
     s += __shfl_xor(s, 2, 64);
     s += __shfl_xor(s, 4, 64);
+    const unsigned st = __shfl(v, kSub, 64);
     if (__builtin_amdgcn_readfirstlane(s) >= target) return true;
-    const unsigned st = ld_agent(g.status);
     if (__builtin_amdgcn_readfirstlane(st) != 0u) return false;
     if (n >= kSpin) {
       if (lane == 0)
@@ -188,64 +220,101 @@ __device__ bool wait_phase(const XArgs& g, int row, unsigned target) {
 
 // ---- GEMM units ---------------------------------------------------------------
 struct GemmRegs {
-  bf16x8 fw[XKS];     // weights of the current unit: this wave's k-steps
   bf16x8 fx[XKS][4];  // activations: this wave's k-steps x 4 row tiles
   float ss[4];        // norm: this lane's row sums of squares (rows tm*16 + fr)
+};
+
+// LDS image of one wave's weight fragments: k-step j of the unit's 16 rows,
+// 64 bytes per row, 16-byte chunk c of row r at slot c ^ ((r >> 1) & 3)
+// (the 16 rows of a fragment read then spread over the banks)
+constexpr int XWSTEP = 16 * 32;  // bf16 per k-step
+__device__ __forceinline__ int wswz(int r, int c) { return c ^ ((r >> 1) & 3); }
+typedef __attribute__((address_space(3))) bf16* lds_bf16p;
+
+// bf16 activations passed between GEMM phases (GEMM inputs, residuals and
+// the attention output) are stored fragment-major: the 16-row x 32-k
+// B-operand fragment of (k-step k / 32, row tile m / 16) is one contiguous,
+// lane-ordered 1 KB block (lane = m % 16 + 16 ((k / 8) % 4), 8 k per lane).
+// A fragment load is then 8 whole cache lines; a row-major fragment touches
+// 16 half-used lines, and a CU's L1 serves misses at a per-line rate (about
+// half the bytes per second).  64 rows (the row limit of this kernel), so a
+// K-column activation takes ceil(K / 32) * 4 KB.
+__device__ __forceinline__ unsigned frag_off(int m, int k) {
+  return ((((unsigned)k >> 5) * 4u + ((unsigned)m >> 4)) * 64u + (unsigned)(m & 15) +
+          16u * (((unsigned)k >> 3) & 3u)) * 8u + ((unsigned)k & 7u);
+}
+
+// epilogue operands, loaded with the activations
+struct EpiPre {
+  f32x4 u, w;      // fp32 bias | RoPE cos, sin | Euler x
+  bf16x4 b, r;     // bf16 bias, residual
 };
 
 __device__ __forceinline__ bool paired(int epi) { return epi == XE_ROPE || epi == XE_SILU; }
 
 // first packed column of unit column tile ct (16-column tile; a paired tile
 // holds 8 columns of a first half and their 8 partners 32 columns on)
-__device__ __forceinline__ int tile_base(const XPhase& P, int ct) {
+__device__ __forceinline__ int tile_base(int epi, int ct) {
   const int n0 = ct * XBN;
-  return paired(P.epi) ? (n0 >> 6) * 64 + ((n0 & 63) >> 4) * 8 : n0;
+  return paired(epi) ? (n0 >> 6) * 64 + ((n0 & 63) >> 4) * 8 : n0;
 }
 
-// This wave's k-steps: [ks0, ks0 + kcnt) of the nks = ceil(K / 32) steps,
-// `per` (uniform) per wave, taken in passes of XKS.
-__device__ __forceinline__ void wave_krange(int K, int wave, int& ks0, int& kcnt, int& per) {
+// This wave's k-steps: [ks0, ks0 + kcnt) of the ceil(K / 32) steps.
+__device__ __forceinline__ void wave_krange(int K, int wave, int& ks0, int& kcnt) {
   const int nks = (K + 31) / 32;
-  per = (nks + XW - 1) / XW;
+  const int per = (nks + XW - 1) / XW;
   ks0 = wave * per;
   kcnt = max(0, min(per, nks - ks0));
 }
-__device__ __forceinline__ int n_passes(int K) {
-  const int per = ((K + 31) / 32 + XW - 1) / XW;
-  return (per + XKS - 1) / XKS;
-}
 
-// Weight fragments of column tile ct for pass `pass` (this lane's row, this
-// wave's k-steps); steps past the wave's range reload its last one (never
-// used), so all XKS loads are issued unconditionally and fly together.
-__device__ __forceinline__ void load_w(const XPhase& P, int ct, int pass, GemmRegs& r) {
+// Weight fragments of column tile ct for this wave's k-steps, streamed into
+// the wave's own LDS region by LDS-DMA (no registers held while they fly;
+// only this wave reads them, after its own vmcnt wait).  Lane l fetches row
+// l / 4 (through the paired-tile row map), chunk wswz(row, l % 4).  Only the
+// wave's own k-steps are requested: a CU holds a bounded number of misses in
+// flight, and repeated requests of one line use them up.  Chunks past K hold
+// other weights: the activations there are zero.
+__device__ __forceinline__ void dma_w(int epi, const bf16* W, int N, int K, int ldw, int ct,
+                                      bf16* sw) {
   const int lane = threadIdx.x & 63, wave = wave_id();
-  const int fr = lane & 15, fk = (lane >> 4) * 8;
-  int ks0, kcnt, per;
-  wave_krange(P.K, wave, ks0, kcnt, per);
-  const int nks = (P.K + 31) / 32;
-  const int base = tile_base(P, ct);
-  const int row = paired(P.epi) ? base + (fr & 7) + (fr >> 3) * 32 : min(base + fr, P.N - 1);
-  const unsigned roff = (unsigned)row * (unsigned)P.ldw;
+  int ks0, kcnt;
+  wave_krange(K, wave, ks0, kcnt);
+  const int base = tile_base(epi, ct);
+  const int r = lane >> 2;
+  const int row = paired(epi) ? base + (r & 7) + (r >> 3) * 32 : min(base + r, N - 1);
+  const int chunk = wswz(r, lane & 3);
+  const bf16* src = W + (long)row * ldw + chunk * 8;
 #pragma unroll
   for (int j = 0; j < XKS; ++j) {
-    const int ks = min(ks0 + min(pass * XKS + j, max(kcnt - 1, 0)), nks - 1);
-    r.fw[j] = ldg8(P.w + (roff + (unsigned)min(ks * 32 + fk, P.K - 8)));
+    if (j >= kcnt) break;  // wave-uniform
+    const int ks = ks0 + j;
+    __builtin_amdgcn_global_load_lds((void*)(src + min(ks * 32, K - 8 - chunk * 8)),
+                                     (lds_ptr_t)(sw + j * XWSTEP), 16, 0, 0);
   }
 }
 
-// Activation fragments of row block rb for pass `pass` (+ the fused norm:
-// gain applied, row sums of squares accumulated); k past K reads as zero.
-__device__ __forceinline__ void load_x(const XPhase& P, int rb, int pass, GemmRegs& r) {
+// Norm gains of this wave's k range (at most XKS * 32 = 256 of them) into
+// the wave's gain row: one DMA instruction, issued before the phase wait.
+__device__ __forceinline__ void dma_gain(const bf16* norm_w, int K, bf16* gain) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  int ks0, kcnt;
+  wave_krange(K, wave, ks0, kcnt);
+  if (kcnt == 0) return;  // wave-uniform
+  __builtin_amdgcn_global_load_lds((void*)(norm_w + min(ks0 * 32 + lane * 8, K - 8)),
+                                   (lds_ptr_t)gain, 16, 0, 0);
+}
+
+// Activation fragments (rows 0..63, clamped to M - 1) of this wave's k-steps
+// (only those: steps past the range are never requested); k past K reads as
+// zero.
+__device__ __forceinline__ void load_x(CPhase& P, GemmRegs& r, const bf16* gain, int t0, int t1) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int fr = lane & 15, fk = (lane >> 4) * 8;
-  int ks0, kcnt, per;
-  wave_krange(P.K, wave, ks0, kcnt, per);
-  const int nks = (P.K + 31) / 32;
-  const int j0 = pass * XKS;
+  int ks0, kcnt;
+  wave_krange(P.K, wave, ks0, kcnt);
   unsigned rows[4];
 #pragma unroll
-  for (int tm = 0; tm < 4; ++tm) rows[tm] = (unsigned)min(rb * XBM + tm * 16 + fr, P.M - 1);
+  for (int tm = 0; tm < 4; ++tm) rows[tm] = (unsigned)min(tm * 16 + fr, P.M - 1);
   if (P.a_f32) {
     // fp32 A (the Euler state into action_in, K <= 32: one k-step, wave 0),
     // rounded to bf16 on the way in
@@ -253,132 +322,175 @@ __device__ __forceinline__ void load_x(const XPhase& P, int rb, int pass, GemmRe
     for (int j = 0; j < XKS; ++j)
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) r.fx[j][tm] = bf16x8{};
-    if (kcnt > 0 && pass == 0) {
+    if (kcnt > 0) {
       const int k = ks0 * 32 + fk;
+      // every load issued before any use (a use right after its load would
+      // make each load a round trip of its own)
+      f32x4 lo[4], hi[4];
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
         const float* src = static_cast<const float*>(P.a) + (rows[tm] * (unsigned)P.lda + (unsigned)min(k, P.K - 8));
-        const f32x4 lo = ldgf4(src);
-        const f32x4 hi = ldgf4(src + 4);
+        lo[tm] = ldgf4(src);
+        hi[tm] = ldgf4(src + 4);
+      }
+#pragma unroll
+      for (int tm = 0; tm < 4; ++tm) {
         bf16x8 t;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) { t[i] = f2bf(lo[i]); t[4 + i] = f2bf(hi[i]); }
+        for (int i = 0; i < 4; ++i) { t[i] = f2bf(lo[tm][i]); t[4 + i] = f2bf(hi[tm][i]); }
         r.fx[0][tm] = k < P.K ? t : bf16x8{};
       }
     }
   } else {
+    // fragment-major A: one contiguous 1 KB block per (k-step, row tile).
+    // Rows past M and k past K are never written (the workspace is cleared
+    // at set-up), so they read as zero and the loads need no select: a use
+    // right after a load would make every load a round trip of its own.
 #pragma unroll
     for (int j = 0; j < XKS; ++j) {
-      const int k = min(ks0 + min(j0 + j, max(kcnt - 1, 0)), nks - 1) * 32 + fk;
-      const int kc = min(k, P.K - 8);
+      if (j >= kcnt) break;  // wave-uniform: no request past the wave's range
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
-        const bf16x8 t = ldg8(static_cast<const bf16*>(P.a) + (rows[tm] * (unsigned)P.lda + (unsigned)kc));
-        r.fx[j][tm] = k < P.K ? t : bf16x8{};
+        if (tm < t0 || tm >= t1) continue;  // wave-uniform: another unit's rows
+        r.fx[j][tm] = ldg8(static_cast<const bf16*>(P.a) + (((unsigned)(ks0 + j) * 4u + tm) * 64u + lane) * 8u);
       }
     }
   }
+#pragma unroll
+  for (int tm = 0; tm < 4; ++tm) r.ss[tm] = 0.f;
   if (P.norm_w) {
+    // the gains' DMA (issued before the phase wait) and the activations landed
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(wc_vm(0));
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
 #pragma unroll
     for (int j = 0; j < XKS; ++j) {
-      if (j0 + j >= kcnt) continue;  // wave-uniform
-      const int k = (ks0 + j0 + j) * 32 + fk;
-      const bf16x8 gv = ldg8(P.norm_w + min(k, P.K - 8));
+      if (j >= kcnt) continue;  // wave-uniform
+      const bf16x8 gv = *reinterpret_cast<const bf16x8*>(gain + j * 32 + fk);
 #pragma unroll
-      for (int tm = 0; tm < 4; ++tm)
+      for (int tm = 0; tm < 4; ++tm) {
+        if (tm < t0 || tm >= t1) continue;  // wave-uniform
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float xv = bf2f(r.fx[j][tm][e]);
           r.ss[tm] = __builtin_fmaf(xv, xv, r.ss[tm]);
           r.fx[j][tm][e] = f2bf(__fmul_rn(xv, bf2f(gv[e])));
         }
+      }
     }
   }
 }
 
-struct XShared {
-  float part[XW][XBM * XPS];  // partial tiles of the 8 waves
-  float ss[XW][XBM];          // per-wave row sums of squares
-  float rs[XBM];              // row scale 1 / rms
-  bf16 vt[XBM][XVT];          // attention: V^T of one head group, [d][key]
-  int rank;
+// Epilogue work item of thread tid in a unit: tile row ml, 4-column group
+// gi, first packed column n; `on` false if the thread has none.
+struct EpiItem {
+  int ml, n, gi;
+  bool on;
 };
 
-template <int ACT>
-__device__ __forceinline__ float xact(float v) {
-  if constexpr (ACT == SVLA_ACT_SILU) return silu_f(v);
-  else if constexpr (ACT == SVLA_ACT_GELU_TANH) return gelu_tanh_f(v);
-  else return v;
+__device__ __forceinline__ bool vt_unit(CPhase& P, int ct) {
+  return P.vt && tile_base(P.epi, ct) >= P.rope_cols;
 }
 
-// The epilogue of one unit (partial tiles already in LDS): sums the 8 waves'
-// tiles in wave order and stores through to memory.
-__device__ void gemm_epilogue(const XPhase& P, int rb, int ct, XShared& sh) {
+__device__ __forceinline__ EpiItem epi_item(CPhase& P, int ct, int t0, int t1) {
   const int tid = threadIdx.x;
-  const int base = tile_base(P, ct);
-  const bool pr = paired(P.epi);
-  const int groups = pr ? XBM * 2 : XBM * (XBN / 4);
-  if (tid >= groups) return;
-  const int ml = pr ? tid >> 1 : tid >> 2;
-  const int gi = pr ? tid & 1 : tid & 3;
-  const int m = rb * XBM + ml;
-  if (m >= P.M) return;
-  auto sum4 = [&](int nl, float v[4]) {
-    f32x4 t = *reinterpret_cast<const f32x4*>(&sh.part[0][ml * XPS + nl]);
+  EpiItem it{};
+  const int base = tile_base(P.epi, ct);
+  if (paired(P.epi)) {
+    it.ml = tid >> 1;
+    it.gi = tid & 1;
+    it.on = tid < XBM * 2 && it.ml < P.M;
+  } else {
+    it.ml = tid >> 2;
+    it.gi = tid & 3;
+    it.on = tid < XBM * 4 && it.ml < P.M;
+  }
+  it.n = base + it.gi * 4;
+  if (!paired(P.epi) && it.n >= P.N) it.on = false;
+  if ((it.ml >> 4) < t0 || (it.ml >> 4) >= t1) it.on = false;  // another unit's rows
+  return it;
+}
+
+// Operands of the epilogue item (addresses clamped into the tensors, so
+// every thread loads; values of threads without an item are ignored).
+__device__ __forceinline__ void epi_prefetch(CPhase& P, const EpiItem& it, EpiPre& e) {
+  const int m = min(it.ml, P.M - 1);
+  const int n = min(it.n, P.N - 4);
+  if (P.epi == XE_STORE) {
+    if (P.bias) e.b = ldg4(P.bias + n);
+    if (P.bias_f32) e.u = ldgf4(P.bias_f32 + n);
+    if (P.res) e.r = ldg4(P.res + frag_off(m, n));  // fragment-major
+  } else if (P.epi == XE_ROPE) {
+    const int pos = m % P.rope_period, d = n & 31;
+    e.u = ldgf4(P.cos_t + pos * 32 + d);
+    e.w = ldgf4(P.sin_t + pos * 32 + d);
+  } else if (P.epi == XE_EULER) {
+    e.u = ldgf4(P.x_in + ((unsigned)m * (unsigned)P.N + (unsigned)n));
+  }
+}
+
+union XShared {
+  struct {
+    float part[XW][XBM * XPS];  // partial tiles of the waves
+    float ss[XW][XBM];          // per-wave row sums of squares
+    float rs[XBM];              // row scale 1 / rms
+    bf16 gain[XW][512];         // norm gains of each wave's k range (staged)
+  } g;
+  struct {
+    float amax[XKQ][4][16];     // [key group][query tile][query]
+    float asum[XKQ][4][16];
+    float o[XKQ][4][64][16];    // partial O^T [key group][query tile][d][query]
+    bf16 q[64 * 64];            // staged queries (rows swizzled as K)
+  } a;
+};
+
+__device__ __forceinline__ f32x4 sum_parts(const XShared& sh, int ml, int nl) {
+  f32x4 t = *reinterpret_cast<const f32x4*>(&sh.g.part[0][ml * XPS + nl]);
 #pragma unroll
-    for (int w = 1; w < XW; ++w) t += *reinterpret_cast<const f32x4*>(&sh.part[w][ml * XPS + nl]);
-    const float sc = P.norm_w ? sh.rs[ml] : 1.0f;
+  for (int w = 1; w < XW; ++w) t += *reinterpret_cast<const f32x4*>(&sh.g.part[w][ml * XPS + nl]);
+  return t;
+}
+
+// The epilogue of one unit (partial tiles in LDS): sums the waves' tiles in
+// wave order and stores through to memory.
+__device__ void gemm_epilogue(CPhase& P, const EpiItem& it, const EpiPre& e,
+                              const XShared& sh) {
+  if (!it.on) return;
+  const int m = it.ml, n = it.n;
+  const float sc = P.norm_w ? sh.g.rs[m] : 1.0f;
+  auto get = [&](int nl, float v[4]) {
+    const f32x4 t = sum_parts(sh, m, nl);
 #pragma unroll
     for (int i = 0; i < 4; ++i) v[i] = t[i] * sc;
   };
   if (P.epi == XE_STORE) {
-    const int n = base + gi * 4;
-    if (n >= P.N) return;
     float v[4];
-    sum4(gi * 4, v);
-    if (P.bias) {
-      const bf16x4 b = ldg4(P.bias + n);
+    get(it.gi * 4, v);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] += bf2f(b[i]);
+    for (int i = 0; i < 4; ++i) {
+      if (P.bias) v[i] += bf2f(e.b[i]);
+      if (P.bias_f32) v[i] += e.u[i];
+      v[i] = rbf(v[i]);
     }
-    if (P.bias_f32) {
-      const f32x4 b = ldgf4(P.bias_f32 + n);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] += b[i];
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = rbf(v[i]);
     if (P.act == SVLA_ACT_SILU) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = rbf(xact<SVLA_ACT_SILU>(v[i]));
+      for (int i = 0; i < 4; ++i) v[i] = rbf(silu_f(v[i]));
     }
     if (P.res) {
-      const bf16x4 r = ldg4(P.res + (long)m * P.ldr + n);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = rbf(v[i] + bf2f(r[i]));
+      for (int i = 0; i < 4; ++i) v[i] = rbf(v[i] + bf2f(e.r[i]));
     }
-    st4_wt(static_cast<bf16*>(P.c) + (long)m * P.ldc + n, v);
+    st4_wt(static_cast<bf16*>(P.c) + frag_off(m, n), v);  // fragment-major
   } else if (P.epi == XE_ROPE) {
-    // rotate-half RoPE on the bf16 projection in fp32 (vla/text_encoder_bf16.py:92-104);
-    // columns past rope_cols (V) are stored as projected
-    const int n = base + gi * 4;
-    float x1[4], x2[4];
-    sum4(gi * 4, x1);
-    sum4(8 + gi * 4, x2);
-    float o1[4], o2[4];
-    if (n < P.rope_cols) {
-      const int pos = m % P.rope_period, d = n & 63;
-      const f32x4 c = ldgf4(P.cos_t + pos * 32 + d);
-      const f32x4 s = ldgf4(P.sin_t + pos * 32 + d);
+    // rotate-half RoPE on the bf16 projection in fp32 (vla/text_encoder_bf16.py:92-104)
+    float x1[4], x2[4], o1[4], o2[4];
+    get(it.gi * 4, x1);
+    get(8 + it.gi * 4, x2);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float a = rbf(x1[i]), b = rbf(x2[i]);
-        o1[i] = __fsub_rn(__fmul_rn(a, c[i]), __fmul_rn(b, s[i]));
-        o2[i] = __fadd_rn(__fmul_rn(b, c[i]), __fmul_rn(a, s[i]));
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) { o1[i] = rbf(x1[i]); o2[i] = rbf(x2[i]); }
+    for (int i = 0; i < 4; ++i) {
+      const float a = rbf(x1[i]), b = rbf(x2[i]);
+      o1[i] = __fsub_rn(__fmul_rn(a, e.u[i]), __fmul_rn(b, e.w[i]));
+      o2[i] = __fadd_rn(__fmul_rn(b, e.u[i]), __fmul_rn(a, e.w[i]));
     }
     bf16* crow = static_cast<bf16*>(P.c) + (long)m * P.ldc;
     st4_wt(crow + n, o1);
@@ -386,39 +498,74 @@ __device__ void gemm_epilogue(const XPhase& P, int rb, int ct, XShared& sh) {
   } else if (P.epi == XE_SILU) {
     // bf16(silu(bf16(gate))) * bf16(up), output column (n / 64) * 32 + n % 64
     // (vla/text_encoder_bf16.py:130-131)
-    const int n = base + gi * 4;
     float g[4], u[4], o[4];
-    sum4(gi * 4, g);
-    sum4(8 + gi * 4, u);
+    get(it.gi * 4, g);
+    get(8 + it.gi * 4, u);
 #pragma unroll
     for (int i = 0; i < 4; ++i) o[i] = rbf(silu_f(rbf(g[i]))) * rbf(u[i]);
-    st4_wt(static_cast<bf16*>(P.c) + (long)m * P.ldc + (n >> 6) * 32 + (n & 63), o);
+    st4_wt(static_cast<bf16*>(P.c) + frag_off(m, (n >> 6) * 32 + (n & 63)), o);  // fragment-major
   } else {
     // Euler: x_out = x_in + dt * bf16(v) in fp32
-    const int n = base + gi * 4;
-    if (n >= P.N) return;
-    float v[4];
-    sum4(gi * 4, v);
-    const f32x4 x = ldgf4(P.x_in + (long)m * P.N + n);
-    float o[4];
+    float v[4], o[4];
+    get(it.gi * 4, v);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = __fadd_rn(x[i], __fmul_rn(P.dt, rbf(v[i])));
+    for (int i = 0; i < 4; ++i) o[i] = __fadd_rn(e.u[i], __fmul_rn(P.dt, rbf(v[i])));
     st2f_wt(P.x_out + (long)m * P.N + n, o[0], o[1]);
     st2f_wt(P.x_out + (long)m * P.N + n + 2, o[2], o[3]);
   }
 }
 
-// acc += this pass's weight and activation fragments
-__device__ __forceinline__ void gemm_mma(const XPhase& P, const GemmRegs& r, int pass, f32x4 (&acc)[4]) {
-  const int wave = wave_id();
-  int ks0, kcnt, per;
-  wave_krange(P.K, wave, ks0, kcnt, per);
+// one V^T word: item = (sample b, key quad kq, tile column c)
+__device__ __forceinline__ void vt_item(CPhase& P, int ct, const XShared& sh, int item) {
+  const int c = item & 15, kq = (item >> 4) & 15, b = item >> 8;
+  const int base = tile_base(P.epi, ct);
+  const int col = (c < 8 ? base + c : base + 32 + (c - 8)) - P.rope_cols;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = 4 * kq + i;
+    float t = 0.f;
+    if (key < P.chunk) {
+      const int ml = b * P.chunk + key;
+#pragma unroll
+      for (int w = 0; w < XW; ++w) t += sh.g.part[w][ml * XPS + c];
+      t = rbf(t * (P.norm_w ? sh.g.rs[ml] : 1.0f));
+    }
+    v[i] = t;
+  }
+  st4_wt(P.vt + ((long)b * (P.N - P.rope_cols) + col) * XVTS + 4 * kq, v);
+}
+
+// V columns of a self layer's QKV projection, stored transposed: thread
+// (tile column c, key quad kq, sample b) stores keys 4 kq .. 4 kq + 3 of
+// column c as one 8-byte word of V^T[b][col][XVTS] (keys past the chunk: 0).
+// V is stored as projected (no RoPE).
+// (several row groups only at one sample: key = row, so a 4-key word lies in
+// one row tile)
+__device__ void vt_epilogue(CPhase& P, int ct, const XShared& sh, int t0, int t1) {
+  const int nb = P.M / P.chunk;
+  for (int item = threadIdx.x; item < 256 * nb; item += XT) {
+    const int tile = ((item >> 4) & 15) >> 2;  // row tile of key 4 kq at sample 0
+    if (P.row_groups > 1 && (tile < t0 || tile >= t1)) continue;
+    vt_item(P, ct, sh, item);
+  }
+}
+
+
+__device__ __forceinline__ void gemm_mma(CPhase& P, const GemmRegs& r, const bf16* sw,
+                                         f32x4 (&acc)[4], int t0, int t1) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int fr = lane & 15, G = lane >> 4;
+  int ks0, kcnt;
+  wave_krange(P.K, wave, ks0, kcnt);
 #pragma unroll
   for (int j = 0; j < XKS; ++j) {
-    if (pass * XKS + j >= kcnt) break;  // wave-uniform
+    if (j >= kcnt) break;  // wave-uniform
+    const bf16x8 fw = *reinterpret_cast<const bf16x8*>(sw + j * XWSTEP + fr * 32 + wswz(fr, G) * 8);
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm)
-      acc[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(r.fw[j], r.fx[j][tm], acc[tm], 0, 0, 0);
+      if (tm >= t0 && tm < t1)  // wave-uniform
+        acc[tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw, r.fx[j][tm], acc[tm], 0, 0, 0);
   }
 }
 
@@ -428,117 +575,291 @@ __device__ __forceinline__ void put_partial(const f32x4 (&acc)[4], XShared& sh) 
   const int fr = lane & 15;
 #pragma unroll
   for (int tm = 0; tm < 4; ++tm)
-    *reinterpret_cast<f32x4*>(&sh.part[wave][(tm * 16 + fr) * XPS + 4 * (lane >> 4)]) = acc[tm];
+    *reinterpret_cast<f32x4*>(&sh.g.part[wave][(tm * 16 + fr) * XPS + 4 * (lane >> 4)]) = acc[tm];
 }
 
 // ---- attention units -----------------------------------------------------------
-// One (sample, head): queries on waves 0..3 (16 each), all 8 waves stage V^T.
-__device__ void attn_unit(const XPhase& P, int unit, XShared& sh) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int b = unit / P.heads, h = unit - b * P.heads;
-  const int g = h * P.kv_heads / P.heads;
+// One (sample, head).  K rows, V^T rows and the queries are staged into LDS by
+// LDS-DMA, each line requested once per CU (fragments loaded straight from
+// memory by every wave would request the same lines several times, and a CU
+// holds a bounded number of misses in flight).  K and V^T use the GEMM weight
+// region (free during attention phases); 16-byte chunks are XOR-swizzled by
+// row so the fragment reads of 16 rows spread over the banks.  Wave w then
+// takes key quarter kq = w % 4 (keys 64 kq .. 64 kq + 63) and the XQT query
+// tiles of query group w / 4.
+
+// 128-byte rows (K, queries; V^T of 64 keys): chunk c of row r at slot
+// c ^ ((r >> 1) & 7); longer V^T rows (128 or 256 keys): c ^ (r & 15)
+__device__ __forceinline__ int rswz8(int r, int c) { return c ^ ((r >> 1) & 7); }
+__device__ __forceinline__ int vswz(int d, int c, int ldvt) {
+  return ldvt <= 64 ? rswz8(d, c) : c ^ (d & 15);
+}
+constexpr int kAttnVt = XMAXK * 64;  // V^T offset in the staging region (bf16)
+
+// K (keys clamped to Lk - 1) and V^T (64 rows of ldvt keys; the writers zero
+// the keys past Lk) of sample b, kv head g: 1 KB per DMA instruction, the
+// instructions dealt round the waves
+__device__ __forceinline__ void attn_stage_kv(CPhase& P, int b, int g, bf16* st) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const bf16* kb = P.k + b * P.k_bs + g * 64;
-  const bf16* vb = P.v + b * P.v_bs + g * 64;
-  const bf16* qb = P.q + b * P.q_bs + h * 64;
-  const int Lk = P.lk, Lq = P.lq;
-  // V^T into LDS: [d][key], keys >= Lk zero
-  for (int idx = tid; idx < XMAXK * 8; idx += XT) {
-    const int key = idx >> 3, d8 = (idx & 7) * 8;
-    bf16x8 val = bf16x8{};
-    if (key < Lk) val = ldg8(vb + (long)key * P.ldv + d8);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sh.vt[d8 + j][key] = val[j];
+  const int nki = (P.lk + 7) >> 3;
+  for (int i = wave; i < nki; i += XW) {
+    const int key = i * 8 + (lane >> 3);
+    const int c = rswz8(key, lane & 7);
+    __builtin_amdgcn_global_load_lds((void*)(kb + (unsigned)min(key, P.lk - 1) * (unsigned)P.ldk + c * 8),
+                                     (lds_ptr_t)(st + i * 512), 16, 0, 0);
   }
-  wg_sync_lds();
-  if (wave >= 4) return;
+  const bf16* vb = P.vt_in + b * P.vt_bs + (long)g * 64 * P.ldvt;
+  const int lg = 31 - __builtin_clz(P.ldvt);  // ldvt is 64, 128 or 256
+  const int nvi = P.ldvt >> 3;                // 64 ldvt elements / 512 per instruction
+  for (int i = wave; i < nvi; i += XW) {
+    const int e = i * 512 + lane * 8;
+    const int d = e >> lg, cs = (e & (P.ldvt - 1)) >> 3;
+    __builtin_amdgcn_global_load_lds((void*)(vb + (unsigned)d * (unsigned)P.ldvt + vswz(d, cs, P.ldvt) * 8),
+                                     (lds_ptr_t)(st + kAttnVt + i * 512), 16, 0, 0);
+  }
+}
+// the 64 query rows (clamped to chunk - 1) of sample b, head h: one
+// instruction per wave
+__device__ __forceinline__ void attn_stage_q(CPhase& P, int b, int h, bf16* lq) {
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const bf16* qb = P.q + b * P.q_bs + h * 64;
+  const int row = wave * 8 + (lane >> 3);
+  const int c = rswz8(row, lane & 7);
+  __builtin_amdgcn_global_load_lds((void*)(qb + (unsigned)min(row, P.chunk - 1) * (unsigned)P.ldq + c * 8),
+                                   (lds_ptr_t)(lq + wave * 512), 16, 0, 0);
+}
+__device__ __forceinline__ void attn_unit_kv(CPhase& P, int unit, bf16* st) {
+  const int b = unit / P.heads, h = unit - b * P.heads;
+  attn_stage_kv(P, b, h * P.kv_heads / P.heads, st);
+}
+
+// kv_staged: this unit's K and V^T DMA was issued already
+__device__ void attn_unit(CPhase& P, int unit, XShared& sh, bf16* st, bool kv_staged) {
+  constexpr int KT = XKW / 16, KS = XKW / 32;  // key tiles and 32-key steps per wave
+  int lane = threadIdx.x & 63;
+  // opaque: lane-derived constants are recomputed here, not hoisted out of
+  // the phase loop (where they would only be spilled)
+  asm volatile("" : "+v"(lane));
+  const int wave = wave_id();
+  const int kq = wave & (XKQ - 1), qg = wave / XKQ;
+  const int b = unit / P.heads, h = unit - b * P.heads;
   const int G = lane >> 4, col = lane & 15;
-  const int q0 = wave * 16;
-  const int qi = q0 + col;
-  const int qc = min(qi, Lq - 1);
-  bf16x8 qf[2];
+  const int Lq = P.chunk, Lk = P.lk, ldvt = P.ldvt;
+  const int k0 = kq * XKW;
+  const int nkt = min(KT, max(0, (Lk - k0 + 15) / 16));  // key tiles with keys (uniform)
+  if (!kv_staged) attn_unit_kv(P, unit, st);
+  attn_stage_q(P, b, h, sh.a.q);
+  // every wave's DMA landed, then the staged rows are visible to all
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(wc_vm(0));
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  const bf16* lk = st;
+  const bf16* lv = st + kAttnVt;
+  int qt[XQT], qc[XQT];
 #pragma unroll
-  for (int ds = 0; ds < 2; ++ds) qf[ds] = ldg8(qb + (long)qc * P.ldq + ds * 32 + G * 8);
-  const int nkt = (Lk + 15) / 16;
-  // S^T tiles: lane holds scores of keys kt*16 + 4G + i for query qi
-  f32x4 s[XMAXK / 16];
+  for (int t = 0; t < XQT; ++t) {
+    qt[t] = qg * XQT + t;
+    qc[t] = min(qt[t] * 16 + col, Lq - 1);
+  }
+  bf16x8 qf[XQT][2];
 #pragma unroll
-  for (int kt = 0; kt < XMAXK / 16; ++kt) {
-    s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (kt >= nkt) continue;  // wave-uniform
-    const int key = min(kt * 16 + col, Lk - 1);
+  for (int t = 0; t < XQT; ++t)
 #pragma unroll
     for (int ds = 0; ds < 2; ++ds) {
-      const bf16x8 kf = ldg8(kb + (long)key * P.ldk + ds * 32 + G * 8);
-      s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ds], s[kt], 0, 0, 0);
+      const int r = qt[t] * 16 + col;
+      qf[t][ds] = *reinterpret_cast<const bf16x8*>(sh.a.q + r * 64 + rswz8(r, ds * 4 + G) * 8);
+    }
+  // S^T tiles: s[q][t] lane holds scores of keys k0 + 16 t + 4 G + i, query col
+  f32x4 s[XQT][KT];
+#pragma unroll
+  for (int t = 0; t < KT; ++t) {
+#pragma unroll
+    for (int q = 0; q < XQT; ++q) s[q][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (t >= nkt) continue;  // wave-uniform
+    const int key = k0 + t * 16 + col;  // < 256: inside the staged rows
+#pragma unroll
+    for (int ds = 0; ds < 2; ++ds) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(lk + key * 64 + rswz8(key, ds * 4 + G) * 8);
+#pragma unroll
+      for (int q = 0; q < XQT; ++q)
+        s[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[q][ds], s[q][t], 0, 0, 0);
     }
   }
-  // exact softmax in fp32 over the visible keys
-  float mx = -INFINITY;
+  // exact softmax: maxima and sums of the key quarters meet in LDS (keys
+  // past Lk, including rows never staged, are masked before any use)
 #pragma unroll
-  for (int kt = 0; kt < XMAXK / 16; ++kt) {
-    if (kt >= nkt) continue;
+  for (int q = 0; q < XQT; ++q) {
+    float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = kt * 16 + 4 * G + i;
-      const bool vis = key < Lk && !(P.causal && key > qc);
-      s[kt][i] = vis ? s[kt][i] * P.scale : -INFINITY;
-      mx = fmaxf(mx, s[kt][i]);
-    }
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = k0 + t * 16 + 4 * G + i;
+        const bool vis = key < Lk && !(P.causal && key > qc[q]);
+        s[q][t][i] = vis ? s[q][t][i] * P.scale : -INFINITY;
+        mx = fmaxf(mx, s[q][t][i]);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    if (lane < 16) sh.a.amax[kq][qt[q]][lane] = mx;
   }
-  mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-  float sum = 0.f;
+  wg_sync_lds();
+  constexpr float kLog2e = 1.4426950408889634f;
 #pragma unroll
-  for (int kt = 0; kt < XMAXK / 16; ++kt) {
-    if (kt >= nkt) continue;
+  for (int q = 0; q < XQT; ++q) {
+    float m = sh.a.amax[0][qt[q]][col];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float e = s[kt][i] == -INFINITY ? 0.f : expf(s[kt][i] - mx);
-      s[kt][i] = e;
-      sum += e;
-    }
+    for (int j = 1; j < XKQ; ++j) m = fmaxf(m, sh.a.amax[j][qt[q]][col]);
+    float sum = 0.f;
+#pragma unroll
+    for (int t = 0; t < KT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ev =
+            s[q][t][i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((s[q][t][i] - m) * kLog2e);
+        s[q][t][i] = ev;
+        sum += ev;
+      }
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    if (lane < 16) sh.a.asum[kq][qt[q]][lane] = sum;
   }
-  sum += __shfl_xor(sum, 16, 64);
-  sum += __shfl_xor(sum, 32, 64);
-  const float inv = 1.0f / sum;
-  // O^T = V^T . P^T over 32-key steps; contraction index 8G + j <-> key
+  wg_sync_lds();
+  // O^T = V^T . P^T over 32-key steps; contraction index 8 G + j <-> key
   // 32 ks + 16 (j / 4) + 4 G + j % 4 (both operands)
-  f32x4 o[4];
+  f32x4 o[XQT][4];
 #pragma unroll
-  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < XQT; ++q)
 #pragma unroll
-  for (int ks = 0; ks < XMAXK / 32; ++ks) {
+    for (int dt = 0; dt < 4; ++dt) o[q][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float inv[XQT];
+#pragma unroll
+  for (int q = 0; q < XQT; ++q) {
+    float l = sh.a.asum[0][qt[q]][col];
+#pragma unroll
+    for (int j = 1; j < XKQ; ++j) l += sh.a.asum[j][qt[q]][col];
+    inv[q] = l;
+  }
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
     if (2 * ks >= nkt) continue;  // wave-uniform
-    bf16x8 pf;
+    const int kk = k0 + 32 * ks + 4 * G;  // < ldvt here
+    bf16x8 pf[XQT];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      pf[i] = f2bf(s[2 * ks][i] / sum);
-      pf[4 + i] = f2bf(s[2 * ks + 1][i] / sum);
-    }
+    for (int q = 0; q < XQT; ++q)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pf[q][i] = f2bf(s[q][2 * ks][i] / inv[q]);
+        pf[q][4 + i] = f2bf(s[q][2 * ks + 1][i] / inv[q]);
+      }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const int d = dt * 16 + col;
-      const uint64_t lo = *reinterpret_cast<const uint64_t*>(&sh.vt[d][32 * ks + 4 * G]);
-      const uint64_t hi = *reinterpret_cast<const uint64_t*>(&sh.vt[d][32 * ks + 16 + 4 * G]);
+      const bf16* row = lv + d * ldvt;
+      const uint64_t lo = *reinterpret_cast<const uint64_t*>(row + vswz(d, kk >> 3, ldvt) * 8 + (kk & 7));
+      const uint64_t hi =
+          *reinterpret_cast<const uint64_t*>(row + vswz(d, (kk + 16) >> 3, ldvt) * 8 + (kk & 7));
       const u32x4 w4 = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
-      const bf16x8 vf = __builtin_bit_cast(bf16x8, w4);
-      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf, o[dt], 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < XQT; ++q)
+        o[q][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w4), pf[q],
+                                                           o[q][dt], 0, 0, 0);
     }
   }
-  (void)inv;
-  if (qi < Lq) {
-    bf16* orow = P.o + b * P.o_bs + (long)qi * P.ldo + h * 64;
+  // partial O^T of this key quarter: lane holds O^T[dt*16 + 4G + i][col]
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt) {
-      float r[4] = {o[dt][0], o[dt][1], o[dt][2], o[dt][3]};
-      st4_wt(orow + dt * 16 + 4 * G, r);
+  for (int q = 0; q < XQT; ++q)
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sh.a.o[kq][qt[q]][dt * 16 + 4 * G + i][col] = o[q][dt][i];
+  wg_sync_lds();
+  // the waves of key quarter 0 sum the quarters in order and store
+  if (kq == 0) {
+#pragma unroll
+    for (int q = 0; q < XQT; ++q) {
+      const int qi = qt[q] * 16 + col;
+      if (qi >= Lq) continue;
+      const int om = b * P.chunk + qi;  // row of the fragment-major output
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        float r[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = dt * 16 + 4 * G + i;
+          float t = sh.a.o[0][qt[q]][d][col];
+#pragma unroll
+          for (int j = 1; j < XKQ; ++j) t += sh.a.o[j][qt[q]][d][col];
+          r[i] = t;
+        }
+        st4_wt(P.o + frag_off(om, h * 64 + dt * 16 + 4 * G), r);
+      }
     }
+  }
+}
+
+// V^T of the cross layers' projected prefix V: unit (layer, sample, block of
+// 64 columns); thread (column d, key quad) for 4 rounds of 64 keys.
+__device__ void vt_unit_transpose(CPhase& P, int unit) {
+  const int tid = threadIdx.x;
+  const int per_layer = P.vt_blocks * (P.M / P.chunk);
+  const int li = unit / per_layer, rem = unit - li * per_layer;
+  const int b = rem / P.vt_blocks, blk = rem - b * P.vt_blocks;
+  const int d = tid & 63, kq = tid >> 6;
+  constexpr int kRound = XT / 64 * 4;  // keys per round
+  const bf16* src = P.vt_src[li] + b * P.vt_src_bs + blk * 64 + d;
+  bf16* dst = P.vt_dst[li] + b * P.vt_dst_bs + (long)(blk * 64 + d) * XMAXK;
+  constexpr int kRounds = XMAXK / kRound;
+  // every load issued before any use (a use right after its load would make
+  // each load a round trip of its own)
+  uint16_t hv[kRounds][4];
+#pragma unroll
+  for (int round = 0; round < kRounds; ++round)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = round * kRound + kq * 4 + i;
+      hv[round][i] = ldg16(src + (long)min(key, P.vt_keys - 1) * P.vt_ldv);
+    }
+#pragma unroll
+  for (int round = 0; round < kRounds; ++round) {
+    const int key0 = round * kRound + kq * 4;
+    uint64_t w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w |= (uint64_t)(key0 + i < P.vt_keys ? hv[round][i] : (uint16_t)0) << (16 * i);
+    st8_wt(dst + key0, w);
   }
 }
 
 // ---- the persistent kernel -------------------------------------------------------
+// Touch every 64-byte line of a phase's table entry with scalar loads, so the
+// reads of its fields after the phase wait hit the scalar cache (a dependent
+// chain of misses would cost a memory round trip per link).  The result only
+// keeps the loads alive.
+__device__ __forceinline__ unsigned touch_phase(CPhase* ph) {
+  typedef const __attribute__((address_space(4))) unsigned cu32;
+  cu32* w = reinterpret_cast<cu32*>(ph);
+  unsigned t = 0;
+#pragma unroll
+  for (int i = 0; i < (int)((sizeof(XPhase) + 63) / 64); ++i) t ^= w[i * 16];
+  return t;
+}
+
+// header fields of a phase used before its wait (read one phase ahead)
+struct Hdr {
+  int kind, epi, units, col_tiles, N, K, ldw;
+  const bf16* w;
+};
+__device__ __forceinline__ Hdr read_hdr(CPhase& P) {
+  return Hdr{P.kind, P.epi, P.units, P.col_tiles, P.N, P.K, P.ldw, P.w};
+}
+
 __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
   __shared__ XShared sh;
+  __shared__ __attribute__((aligned(1024))) bf16 s_w[XW][XKS * XWSTEP];  // per-wave weights
+  __shared__ int s_rank;
   const int tid = threadIdx.x, wave = wave_id(), lane = tid & 63;
   // team: every workgroup, or those on XCD team_xcd (ranked on arrival)
   if (tid == 0) {
@@ -554,10 +875,10 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
         rank = r < (unsigned)g.team_size ? (int)r : -1;
       }
     }
-    sh.rank = rank;
+    s_rank = rank;
   }
   __syncthreads();
-  const int rank = sh.rank;
+  const int rank = s_rank;
   if (rank < 0) return;
   const int team = g.team_xcd >= 0 ? g.team_size : (int)gridDim.x;
   if (g.team_xcd >= 0) {
@@ -566,87 +887,105 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
       const unsigned* reg = g.cnt + (size_t)g.n_ph * kSub * kCntStride;
       bool ok = false;
       for (int n = 0; n < kSpin; ++n) {
-        const unsigned r = __builtin_amdgcn_readfirstlane(ld_agent(reg));
-        if (r >= (unsigned)team) { ok = true; break; }
+        const unsigned rr = __builtin_amdgcn_readfirstlane(ld_agent(reg));
+        if (rr >= (unsigned)team) { ok = true; break; }
         if (__builtin_amdgcn_readfirstlane(ld_agent(g.status)) != 0u) break;
       }
       if (!ok && lane == 0)
         __hip_atomic_store(g.status, (unsigned)XS_TEAM, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (lane == 0) sh.rank = ok ? rank : -1;
+      if (lane == 0) s_rank = ok ? rank : -1;
     }
     __syncthreads();
-    if (sh.rank < 0) return;
+    if (s_rank < 0) return;
   }
 
+  Hdr h = read_hdr(g.ph[0]);
   for (int p = 0; p < g.n_ph; ++p) {
-    const XPhase& P = g.ph[p];
-    const int units = P.units;
-    if (rank >= units) continue;
+    const Hdr cur = h;
+    if (p + 1 < g.n_ph) h = read_hdr(g.ph[p + 1]);  // next phase's header, early
+    if (rank >= cur.units) continue;
+    CPhase& P = g.ph[p];
+    const int mine = (cur.units - rank + team - 1) / team;
     GemmRegs r;
-    const int mine = (units - rank + team - 1) / team;
-    const bool gemm = P.kind == XK_GEMM;
-    // weights of the first unit before the wait (they do not depend on it)
-    if (gemm) load_w(P, rank % P.col_tiles, 0, r);
+    bf16* sw = s_w[wave];
+    // weights of the first unit (and the K / V^T of a cross-attention unit)
+    // before the wait: they do not depend on it
+    if (cur.kind == XK_GEMM) {
+      dma_w(cur.epi, cur.w, cur.N, cur.K, cur.ldw, rank % cur.col_tiles, sw);
+      if (P.norm_w) dma_gain(P.norm_w, cur.K, sh.g.gain[wave]);
+    }
+    else if (cur.kind == XK_ATTN && P.kv_static)
+      attn_unit_kv(P, rank, &s_w[0][0]);
     if (p > 0) {
+      if (wave == 1) {
+        // while wave 0 waits: this phase's table entry into the scalar cache
+        const unsigned t = touch_phase(g.ph + p);
+        asm volatile("" ::"s"(t));
+      }
       if (wave == 0) {
         const bool ok = wait_phase(g, p - 1, (unsigned)g.ph[p - 1].units);
-        if (lane == 0) sh.rank = ok ? rank : -1;
+        if (lane == 0) s_rank = ok ? rank : -1;
       }
       __syncthreads();
-      if (sh.rank < 0) return;
+      if (s_rank < 0) return;
     }
-    if (gemm) {
-      const int npass = n_passes(P.K);
-      int rb_loaded = -1;
+    if (cur.kind == XK_GEMM) {
       for (int j = 0; j < mine; ++j) {
         const int u = rank + j * team;
-        const int rb = u / P.col_tiles, ct = u - rb * P.col_tiles;
+        const int ct = u % cur.col_tiles, grp = u / cur.col_tiles;
+        const int t0 = grp * P.group_tiles, t1 = min(t0 + P.group_tiles, 4);
+        const bool vt = vt_unit(P, ct);
+        const EpiItem it = epi_item(P, ct, t0, t1);
+        EpiPre e{};
+        if (!vt) epi_prefetch(P, it, e);
+        // one row group: the activations stay in registers for the phase's units
+        const bool load = j == 0 || P.row_groups > 1;
+        if (load) {
+          load_x(P, r, sh.g.gain[wave], t0, t1);
+          if (P.norm_w) {
+            // per-row sums of squares of the whole K range meet in LDS
+#pragma unroll
+            for (int tm = 0; tm < 4; ++tm) {
+              float t = r.ss[tm];
+              t += __shfl_xor(t, 16, 64);
+              t += __shfl_xor(t, 32, 64);
+              if (lane < 16) sh.g.ss[wave][tm * 16 + lane] = t;
+            }
+          }
+        }
         f32x4 acc[4];
 #pragma unroll
         for (int tm = 0; tm < 4; ++tm) acc[tm] = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int pass = 0; pass < npass; ++pass) {
-          if (pass > 0) load_w(P, ct, pass, r);
-          // activations stay in registers across the units of a row block
-          // when one pass covers K
-          if (npass > 1 || rb != rb_loaded) {
-            if (pass == 0) {
-#pragma unroll
-              for (int tm = 0; tm < 4; ++tm) r.ss[tm] = 0.f;
-            }
-            load_x(P, rb, pass, r);
-            rb_loaded = rb;
-          }
-          gemm_mma(P, r, pass, acc);
-        }
-        // the next unit's first weights load during this unit's epilogue
-        if (j + 1 < mine) load_w(P, (u + team) % P.col_tiles, 0, r);
+        // this wave's weight DMA (issued first) and activations have landed
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        __builtin_amdgcn_s_waitcnt(wc_vm(0));
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        gemm_mma(P, r, sw, acc, t0, t1);
         put_partial(acc, sh);
-        if (P.norm_w) {
-          // per-row sums of squares of the whole K range meet in LDS
-#pragma unroll
-          for (int tm = 0; tm < 4; ++tm) {
-            float t = r.ss[tm];
-            t += __shfl_xor(t, 16, 64);
-            t += __shfl_xor(t, 32, 64);
-            if (lane < 16) sh.ss[wave][tm * 16 + lane] = t;
-          }
-          wg_sync_lds();
+        wg_sync_lds();  // also: this wave's weight reads are done
+        // the next unit's weights stream in during this unit's epilogue
+        if (j + 1 < mine)
+          dma_w(cur.epi, cur.w, cur.N, cur.K, cur.ldw, (u + team) % cur.col_tiles, sw);
+        if (load && P.norm_w) {
           if (tid < XBM) {
             float t = 0.f;
 #pragma unroll
-            for (int w = 0; w < XW; ++w) t += sh.ss[w][tid];
-            sh.rs[tid] = 1.0f / sqrtf(t / (float)P.K + P.norm_eps);
+            for (int w = 0; w < XW; ++w) t += sh.g.ss[w][tid];
+            sh.g.rs[tid] = 1.0f / sqrtf(t / (float)P.K + P.norm_eps);
           }
+          wg_sync_lds();
         }
-        wg_sync_lds();
-        gemm_epilogue(P, rb, ct, sh);
+        if (vt) vt_epilogue(P, ct, sh, t0, t1);
+        else gemm_epilogue(P, it, e, sh);
         wg_sync_lds();  // partial tiles free for the next unit
       }
-    } else {
+    } else if (cur.kind == XK_ATTN) {
       for (int j = 0; j < mine; ++j) {
-        attn_unit(P, rank + j * team, sh);
-        wg_sync_lds();  // V^T free for the next unit
+        attn_unit(P, rank + j * team, sh, &s_w[0][0], j == 0 && P.kv_static);
+        wg_sync_lds();  // LDS free for the next unit
       }
+    } else {
+      for (int j = 0; j < mine; ++j) vt_unit_transpose(P, rank + j * team);
     }
     // every store of this workgroup acknowledged, then one arrival
     __builtin_amdgcn_s_waitcnt(wc_vm(0));
@@ -681,22 +1020,32 @@ struct Layout {
   size_t n_cnt_words;
 };
 
-int count_phases(const svla_expert_desc* d) { return d->num_steps * (4 + 5 * d->n_layers); }
+int n_cross(const svla_expert_desc* d) {
+  int n = 0;
+  for (int l = 0; l < d->n_layers; ++l) n += d->layers[l].cross != 0;
+  return n;
+}
+
+int count_phases(const svla_expert_desc* d) {
+  return (n_cross(d) > 0 ? 1 : 0) + d->num_steps * (4 + 5 * d->n_layers);
+}
 
 bool desc_ok(const svla_expert_desc* d) {
-  if (!d || d->batch <= 0 || d->chunk <= 0 || d->chunk > XMAXQ || d->head_dim != 64) return false;
+  if (!d || d->batch <= 0 || d->chunk <= 0 || d->head_dim != 64) return false;
+  if (d->batch * d->chunk > XBM || d->chunk > XVTS) return false;
   if (d->hidden % 16 || d->inter % 32 || d->action_dim % 16 || d->n_layers <= 0) return false;
-  if (d->hidden > XKS * XPASS * XW * 32 || d->inter > XKS * XPASS * XW * 32) return false;
+  if (d->hidden > XKS * XW * 32 || d->inter > XKS * XW * 32 || d->action_dim > 32) return false;
   if (d->n_q_heads <= 0 || d->n_kv_heads <= 0 || d->n_q_heads % d->n_kv_heads) return false;
-  if (d->n_q_heads * 64 > XKS * XPASS * XW * 32) return false;
+  if (d->n_q_heads * 64 > XKS * XW * 32) return false;
   if (d->num_steps <= 0 || d->prefix_len <= 0 || d->prefix_len > XMAXK) return false;
   if (!d->layers || !d->w_action_in || !d->w_time_in_a || !d->time_bias || !d->w_time_out ||
       !d->w_action_out || !d->rope_cos || !d->rope_sin)
     return false;
+  if (n_cross(d) > kMaxCross) return false;
   for (int l = 0; l < d->n_layers; ++l) {
     const svla_expert_layer& L = d->layers[l];
     if (!L.w_qkv || !L.w_o || !L.w_gu || !L.w_down || !L.norm1 || !L.norm2) return false;
-    if (L.cross && (!L.cross_k || !L.cross_v)) return false;
+    if (L.cross && (!L.cross_k || !L.cross_v || d->ld_cross % 8)) return false;
   }
   return true;
 }
@@ -705,7 +1054,6 @@ bool desc_ok(const svla_expert_desc* d) {
 size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, Layout* lay) {
   const int M = d->batch * d->chunk, H = d->hidden, qd = d->n_q_heads * 64,
             kvd = d->n_kv_heads * 64, I = d->inter, A = d->action_dim;
-  const int rbs = (M + XBM - 1) / XBM;
   Layout L{};
   L.n_ph = count_phases(d);
   L.n_cnt_words = (size_t)(L.n_ph + 1) * kSub * kCntStride;
@@ -718,81 +1066,109 @@ size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, La
     const size_t o = ar.take(bytes);
     return base ? base + o : nullptr;
   };
+  // fragment-major activation of N columns (64 rows)
+  auto fbuf = [&](int N) { return (bf16*)buf((size_t)((N + 31) / 32) * 4096); };
   auto gemm = [&](const void* a, int lda, const void* w, int N, int K, void* c, int ldc) {
     XPhase P{};
     P.kind = XK_GEMM;
     P.epi = XE_STORE;
     P.M = M; P.N = N; P.K = K;
     P.col_tiles = (N + XBN - 1) / XBN;
-    P.units = rbs * P.col_tiles;
+    P.units = P.col_tiles;
     P.a = a; P.lda = lda;
     P.w = static_cast<const bf16*>(w); P.ldw = K;
     P.c = c; P.ldc = ldc;
     P.norm_eps = d->rms_eps;
+    P.chunk = d->chunk;
     return P;
   };
   std::vector<XPhase> ph;
+  // V^T of every cross layer's projected prefix V: [sample][kv][256 keys]
+  std::vector<bf16*> cross_vt(d->n_layers, nullptr);
+  if (n_cross(d) > 0) {
+    XPhase T{};
+    T.kind = XK_VT;
+    T.M = M; T.chunk = d->chunk;
+    T.vt_blocks = kvd / 64;
+    T.vt_ldv = d->ld_cross;
+    T.vt_keys = d->prefix_len;
+    T.vt_src_bs = (long)d->prefix_len * d->ld_cross;
+    T.vt_dst_bs = (long)kvd * XMAXK;
+    for (int l = 0; l < d->n_layers; ++l) {
+      if (!d->layers[l].cross) continue;
+      cross_vt[l] = (bf16*)buf((size_t)d->batch * kvd * XMAXK * 2);
+      T.vt_src[T.n_vt] = static_cast<const bf16*>(d->layers[l].cross_v);
+      T.vt_dst[T.n_vt] = cross_vt[l];
+      ++T.n_vt;
+    }
+    T.units = T.n_vt * d->batch * T.vt_blocks;
+    ph.push_back(T);
+  }
   const float* x_prev = d->x_in;
   for (int s = 0; s < d->num_steps; ++s) {
     // action / time embedding (the time part of time_in precomputed per step)
-    bf16* a_emb = (bf16*)buf((size_t)M * H * 2);
+    bf16* a_emb = fbuf(H);
     XPhase P = gemm(x_prev, A, d->w_action_in, H, A, a_emb, H);
     P.a_f32 = 1;
     P.bias = static_cast<const bf16*>(d->b_action_in);
     ph.push_back(P);
-    bf16* h_t = (bf16*)buf((size_t)M * H * 2);
+    bf16* h_t = fbuf(H);
     P = gemm(a_emb, H, d->w_time_in_a, H, H, h_t, H);
     P.bias_f32 = d->time_bias + (size_t)s * H;
     P.act = SVLA_ACT_SILU;
     ph.push_back(P);
-    bf16* ex = (bf16*)buf((size_t)M * H * 2);
+    bf16* ex = fbuf(H);
     P = gemm(h_t, H, d->w_time_out, H, H, ex, H);
     P.bias = static_cast<const bf16*>(d->b_time_out);
     ph.push_back(P);
     for (int l = 0; l < d->n_layers; ++l) {
       const svla_expert_layer& Ly = d->layers[l];
-      const int nq = Ly.cross ? qd : qd + 2 * kvd;
-      bf16* qkv = (bf16*)buf((size_t)M * nq * 2);
-      P = gemm(ex, H, Ly.w_qkv, nq, H, qkv, nq);
+      const int nq = Ly.cross ? qd : qd + 2 * kvd;  // projected columns
+      const int nqk = Ly.cross ? qd : qd + kvd;     // stored row-major (Q | K)
+      bf16* qk = (bf16*)buf((size_t)M * nqk * 2);
+      bf16* vt = Ly.cross ? nullptr : (bf16*)buf((size_t)d->batch * kvd * XVTS * 2);
+      P = gemm(ex, H, Ly.w_qkv, nq, H, qk, nqk);
       P.epi = XE_ROPE;
       P.norm_w = static_cast<const bf16*>(Ly.norm1);
       P.cos_t = d->rope_cos; P.sin_t = d->rope_sin;
-      P.rope_cols = Ly.cross ? qd : qd + kvd;
+      P.rope_cols = nqk;
       P.rope_period = d->chunk;
+      P.vt = vt;
       ph.push_back(P);
-      bf16* att = (bf16*)buf((size_t)M * qd * 2);
+      bf16* att = fbuf(qd);
       XPhase T{};
       T.kind = XK_ATTN;
+      T.M = M;
       T.units = d->batch * d->n_q_heads;
       T.heads = d->n_q_heads; T.kv_heads = d->n_kv_heads;
-      T.lq = d->chunk;
+      T.chunk = d->chunk;
       T.scale = 0.125f;
-      T.q = qkv; T.ldq = nq; T.q_bs = (long)d->chunk * nq;
+      T.q = qk; T.ldq = nqk; T.q_bs = (long)d->chunk * nqk;
       if (Ly.cross) {
         T.k = static_cast<const bf16*>(Ly.cross_k); T.ldk = d->ld_cross;
-        T.v = static_cast<const bf16*>(Ly.cross_v); T.ldv = d->ld_cross;
-        T.k_bs = T.v_bs = (long)d->prefix_len * d->ld_cross;
+        T.k_bs = (long)d->prefix_len * d->ld_cross;
+        T.vt_in = cross_vt[l]; T.ldvt = XMAXK; T.vt_bs = (long)kvd * XMAXK;
         T.lk = d->prefix_len;
         T.causal = 0;
+        T.kv_static = 1;
       } else {
-        T.k = qkv + qd; T.ldk = nq;
-        T.v = qkv + qd + kvd; T.ldv = nq;
-        T.k_bs = T.v_bs = (long)d->chunk * nq;
+        T.k = qk + qd; T.ldk = nqk; T.k_bs = (long)d->chunk * nqk;
+        T.vt_in = vt; T.ldvt = XVTS; T.vt_bs = (long)kvd * XVTS;
         T.lk = d->chunk;
         T.causal = 1;
       }
       T.o = att; T.ldo = qd; T.o_bs = (long)d->chunk * qd;
       ph.push_back(T);
-      bf16* ex1 = (bf16*)buf((size_t)M * H * 2);
+      bf16* ex1 = fbuf(H);
       P = gemm(att, qd, Ly.w_o, H, qd, ex1, H);
       P.res = ex; P.ldr = H;
       ph.push_back(P);
-      bf16* act = (bf16*)buf((size_t)M * I * 2);
+      bf16* act = fbuf(I);
       P = gemm(ex1, H, Ly.w_gu, 2 * I, H, act, I);
       P.epi = XE_SILU;
       P.norm_w = static_cast<const bf16*>(Ly.norm2);
       ph.push_back(P);
-      bf16* ex2 = (bf16*)buf((size_t)M * H * 2);
+      bf16* ex2 = fbuf(H);
       P = gemm(act, I, Ly.w_down, H, I, ex2, H);
       P.res = ex1; P.ldr = H;
       ph.push_back(P);
@@ -807,6 +1183,21 @@ size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, La
     P.dt = d->dt;
     ph.push_back(P);
     x_prev = x_next;
+  }
+  // Row groups: a phase with few column tiles also splits its row tiles over
+  // units, so a unit reads only its rows' activations (the critical path of
+  // a phase; the weights stream in before the phase wait).  Up to
+  // kUnitTarget units (one per CU of an MI355X); several groups of a phase
+  // writing V^T only at one sample (key = row there).
+  constexpr int kUnitTarget = 256;
+  const int nrt = (M + 15) / 16;
+  for (XPhase& P : ph) {
+    if (P.kind != XK_GEMM) continue;
+    int rg = 1;
+    while (rg * 2 <= nrt && P.col_tiles * rg * 2 <= kUnitTarget && (!P.vt || d->batch == 1)) rg *= 2;
+    P.row_groups = rg;
+    P.group_tiles = rg == 1 ? 4 : (nrt + rg - 1) / rg;
+    P.units = P.col_tiles * rg;
   }
   L.total = ar.off;
   if (out) *out = std::move(ph);
@@ -830,11 +1221,19 @@ int svla_expert_prepare(const svla_expert_desc* d, void* ws, long ws_bytes, int 
     return SVLA_EINVAL;
   std::vector<XPhase> ph;
   Layout L{};
-  if (ws_bytes < 0 || build(d, static_cast<char*>(ws), &ph, &L) > (size_t)ws_bytes) return SVLA_EINVAL;
+  if (ws_bytes < 0 || build(d, static_cast<char*>(ws), &ph, &L) > (size_t)ws_bytes)
+    return SVLA_EINVAL;
+  if ((int)ph.size() != L.n_ph || L.status != L.counters + L.n_cnt_words * 4) return SVLA_EINVAL;
   char* base = static_cast<char*>(ws);
   hipStream_t s = (hipStream_t)stream;
-  hipError_t e = hipMemcpyAsync(base + L.phases, ph.data(), sizeof(XPhase) * ph.size(),
-                                hipMemcpyHostToDevice, s);
+  // zero the whole workspace once: the padding rows and columns of the
+  // fragment-major activations are never written and must read as zero
+  hipLaunchKernelGGL(clear_u32_kernel, dim3(1024), dim3(256), 0, s, reinterpret_cast<unsigned*>(base),
+                     (long)(L.total / 4));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  e = hipMemcpyAsync(base + L.phases, ph.data(), sizeof(XPhase) * ph.size(),
+                     hipMemcpyHostToDevice, s);
   if (e != hipSuccess) return (int)e;
   e = hipStreamSynchronize(s);
   if (e != hipSuccess) return (int)e;
@@ -861,7 +1260,7 @@ int svla_expert_run(const svla_expert_plan* plan, svla_stream_t stream) {
   hipLaunchKernelGGL(clear_u32_kernel, dim3(256), dim3(256), 0, s, plan->counters, words);
   SVLA_CHECK_LAUNCH();
   XArgs g;
-  g.ph = static_cast<const XPhase*>(plan->phases);
+  g.ph = (CPhase*)plan->phases;
   g.n_ph = plan->n_phases;
   g.cnt = plan->counters;
   g.status = plan->status;
