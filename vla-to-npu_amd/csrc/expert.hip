@@ -43,9 +43,10 @@
 //    holds its k-range of the 64 activation rows in registers and streams
 //    its 16x16x32 MFMA weight fragments into a private LDS region by LDS-DMA
 //    (no registers held while they fly); the partial tiles meet in LDS.
-//    The RMSNorm in front of a projection is fused (gain on the way into the
-//    MFMAs, row sums of squares from the same fragments, 1/rms in the
-//    epilogue).  Paired epilogues (RoPE pairs (d, d+32), SiLU(gate) * up) use
+//    The RMSNorm in front of a projection is fused: the gain multiplies the
+//    unit's weight fragments (16 rows of W, where the activations are 64
+//    rows) on the way into the MFMAs, row sums of squares come from the
+//    activation fragments, 1/rms is applied in the epilogue.  Paired epilogues (RoPE pairs (d, d+32), SiLU(gate) * up) use
 //    the 16-column tile of 8 columns + their partners.  The V columns of a
 //    self layer's QKV projection are written transposed (V^T [kv][64 keys])
 //    for the attention.
@@ -77,9 +78,8 @@ constexpr int XBM = 64;            // rows per GEMM unit (4 MFMA row tiles) = ma
 constexpr int XBN = 16;            // columns per GEMM unit
 constexpr int XPS = XBN + 4;       // padded LDS row of a partial tile (floats)
 constexpr int XMAXK = 256;         // attention: keys per sample
-constexpr int XKQ = 4;             // attention: key quarters (waves = XW / 4 query groups x 4)
-constexpr int XKW = XMAXK / XKQ;   // attention: keys per wave (64)
-constexpr int XQT = 4 / (XW / XKQ);  // attention: 16-query tiles per wave
+constexpr int XKW = 64;            // attention: keys of the one-wave-per-query-tile path
+constexpr int XKG = XMAXK / XW;    // attention: keys per wave of the split path (32)
 constexpr int XVTS = 64;           // self-attention V^T: keys per sample (leading dimension)
 constexpr int kMaxCross = 16;      // cross layers (V^T transposes in the first phase)
 constexpr int kSub = 8;            // sub-counters per phase
@@ -123,6 +123,7 @@ struct XPhase {
   int ldq, ldk, ldvt, ldo;
   long q_bs, k_bs, vt_bs, o_bs;
   int heads, kv_heads, lk, causal;
+  int q_tiles;    // units per (sample, head): 16-query tiles, or 1 (every key in one wave)
   int kv_static;  // K and V^T were written before the previous phase (cross layers)
   float scale;
   // V^T transposes (first phase): unit = (layer, sample, 64-column block)
@@ -148,6 +149,7 @@ struct XArgs {
 
 // Loads through pointers read from the phase table: tell the compiler they
 // are global (flat loads would also count on lgkmcnt and force full waits).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef const __attribute__((address_space(1))) bf16x8* gbf8p;
 typedef const __attribute__((address_space(1))) f32x4* gf4p;
 typedef const __attribute__((address_space(1))) bf16x4* gbf4p;
@@ -307,7 +309,7 @@ __device__ __forceinline__ void dma_gain(const bf16* norm_w, int K, bf16* gain) 
 // Activation fragments (rows 0..63, clamped to M - 1) of this wave's k-steps
 // (only those: steps past the range are never requested); k past K reads as
 // zero.
-__device__ __forceinline__ void load_x(CPhase& P, GemmRegs& r, const bf16* gain, int t0, int t1) {
+__device__ __forceinline__ void load_x(CPhase& P, GemmRegs& r, int t0, int t1) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int fr = lane & 15, fk = (lane >> 4) * 8;
   int ks0, kcnt;
@@ -359,22 +361,23 @@ __device__ __forceinline__ void load_x(CPhase& P, GemmRegs& r, const bf16* gain,
 #pragma unroll
   for (int tm = 0; tm < 4; ++tm) r.ss[tm] = 0.f;
   if (P.norm_w) {
-    // the gains' DMA (issued before the phase wait) and the activations landed
+    // per-row sums of squares (the gains go onto the weight fragments in
+    // gemm_mma: 16 rows of W per unit instead of 64 of A); the activations
+    // landed first
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(wc_vm(0));
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 #pragma unroll
     for (int j = 0; j < XKS; ++j) {
       if (j >= kcnt) continue;  // wave-uniform
-      const bf16x8 gv = *reinterpret_cast<const bf16x8*>(gain + j * 32 + fk);
 #pragma unroll
       for (int tm = 0; tm < 4; ++tm) {
         if (tm < t0 || tm >= t1) continue;  // wave-uniform
+        const bf16x8 x = r.fx[j][tm];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float xv = bf2f(r.fx[j][tm][e]);
-          r.ss[tm] = __builtin_fmaf(xv, xv, r.ss[tm]);
-          r.fx[j][tm][e] = f2bf(__fmul_rn(xv, bf2f(gv[e])));
+        for (int e = 0; e < 8; e += 2) {
+          const bf16x2 xp = {x[e], x[e + 1]};
+          r.ss[tm] = __builtin_amdgcn_fdot2_f32_bf16(xp, xp, r.ss[tm], false);
         }
       }
     }
@@ -437,9 +440,9 @@ union XShared {
     bf16 gain[XW][512];         // norm gains of each wave's k range (staged)
   } g;
   struct {
-    float amax[XKQ][4][16];     // [key group][query tile][query]
-    float asum[XKQ][4][16];
-    float o[XKQ][4][64][16];    // partial O^T [key group][query tile][d][query]
+    float amax[XW][16];         // [key group][query]
+    float asum[XW][16];
+    float o[XW][64][16];        // partial O^T [key group][d][query]
     bf16 q[64 * 64];            // staged queries (rows swizzled as K)
   } a;
 };
@@ -552,8 +555,10 @@ __device__ void vt_epilogue(CPhase& P, int ct, const XShared& sh, int t0, int t1
 }
 
 
+// gain: the norm gains of the wave's k range (LDS), or null: the weight
+// fragment is multiplied by them (rounded to bf16) before the MFMA
 __device__ __forceinline__ void gemm_mma(CPhase& P, const GemmRegs& r, const bf16* sw,
-                                         f32x4 (&acc)[4], int t0, int t1) {
+                                         const bf16* gain, f32x4 (&acc)[4], int t0, int t1) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int fr = lane & 15, G = lane >> 4;
   int ks0, kcnt;
@@ -561,7 +566,12 @@ __device__ __forceinline__ void gemm_mma(CPhase& P, const GemmRegs& r, const bf1
 #pragma unroll
   for (int j = 0; j < XKS; ++j) {
     if (j >= kcnt) break;  // wave-uniform
-    const bf16x8 fw = *reinterpret_cast<const bf16x8*>(sw + j * XWSTEP + fr * 32 + wswz(fr, G) * 8);
+    bf16x8 fw = *reinterpret_cast<const bf16x8*>(sw + j * XWSTEP + fr * 32 + wswz(fr, G) * 8);
+    if (gain) {  // uniform
+      const bf16x8 gv = *reinterpret_cast<const bf16x8*>(gain + j * 32 + G * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) fw[e] = f2bf(__fmul_rn(bf2f(fw[e]), bf2f(gv[e])));
+    }
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm)
       if (tm >= t0 && tm < t1)  // wave-uniform
@@ -584,9 +594,11 @@ __device__ __forceinline__ void put_partial(const f32x4 (&acc)[4], XShared& sh) 
 // memory by every wave would request the same lines several times, and a CU
 // holds a bounded number of misses in flight).  K and V^T use the GEMM weight
 // region (free during attention phases); 16-byte chunks are XOR-swizzled by
-// row so the fragment reads of 16 rows spread over the banks.  Wave w then
-// takes key quarter kq = w % 4 (keys 64 kq .. 64 kq + 63) and the XQT query
-// tiles of query group w / 4.
+// row so the fragment reads of 16 rows spread over the banks.  With at most
+// 64 keys a unit is one (sample, head) and wave w < 4 takes query tile w with
+// every key; with more keys a unit is one (sample, head, 16-query tile) -- the
+// softmax is VALU work, so it is spread over 4x the CUs -- and wave w takes
+// keys 32 w .. 32 w + 31, the waves meeting in LDS for the exact softmax.
 
 // 128-byte rows (K, queries; V^T of 64 keys): chunk c of row r at slot
 // c ^ ((r >> 1) & 7); longer V^T rows (128 or 256 keys): c ^ (r & 15)
@@ -619,141 +631,92 @@ __device__ __forceinline__ void attn_stage_kv(CPhase& P, int b, int g, bf16* st)
                                      (lds_ptr_t)(st + kAttnVt + i * 512), 16, 0, 0);
   }
 }
-// the 64 query rows (clamped to chunk - 1) of sample b, head h: one
-// instruction per wave
-__device__ __forceinline__ void attn_stage_q(CPhase& P, int b, int h, bf16* lq) {
+// query rows r0 .. r0 + 8 n - 1 (clamped to chunk - 1) of sample b, head h
+// into LDS rows 0 .. 8 n - 1: one instruction for each of waves 0 .. n - 1
+__device__ __forceinline__ void attn_stage_q(CPhase& P, int b, int h, int r0, int n, bf16* lq) {
   const int lane = threadIdx.x & 63, wave = wave_id();
+  if (wave >= n) return;  // wave-uniform
   const bf16* qb = P.q + b * P.q_bs + h * 64;
   const int row = wave * 8 + (lane >> 3);
   const int c = rswz8(row, lane & 7);
-  __builtin_amdgcn_global_load_lds((void*)(qb + (unsigned)min(row, P.chunk - 1) * (unsigned)P.ldq + c * 8),
+  __builtin_amdgcn_global_load_lds((void*)(qb + (unsigned)min(r0 + row, P.chunk - 1) * (unsigned)P.ldq + c * 8),
                                    (lds_ptr_t)(lq + wave * 512), 16, 0, 0);
 }
+__device__ __forceinline__ void attn_decode(CPhase& P, int unit, int& b, int& h, int& qt) {
+  const int bh = unit / P.q_tiles;
+  qt = unit - bh * P.q_tiles;
+  b = bh / P.heads;
+  h = bh - b * P.heads;
+}
 __device__ __forceinline__ void attn_unit_kv(CPhase& P, int unit, bf16* st) {
-  const int b = unit / P.heads, h = unit - b * P.heads;
+  int b, h, qt;
+  attn_decode(P, unit, b, h, qt);
   attn_stage_kv(P, b, h * P.kv_heads / P.heads, st);
 }
 
-// kv_staged: this unit's K and V^T DMA was issued already
-__device__ void attn_unit(CPhase& P, int unit, XShared& sh, bf16* st, bool kv_staged) {
-  constexpr int KT = XKW / 16, KS = XKW / 32;  // key tiles and 32-key steps per wave
-  int lane = threadIdx.x & 63;
-  // opaque: lane-derived constants are recomputed here, not hoisted out of
-  // the phase loop (where they would only be spilled)
-  asm volatile("" : "+v"(lane));
-  const int wave = wave_id();
-  const int kq = wave & (XKQ - 1), qg = wave / XKQ;
-  const int b = unit / P.heads, h = unit - b * P.heads;
+// Every key in one 64-key quarter (self-attention over one chunk): wave qt
+// of 0..3 takes query tile qt with all keys, so maxima, sums and the output
+// stay in the wave (the same sums as the quarter exchange, whose other
+// quarters add nothing).
+__device__ __forceinline__ void attn_solo(CPhase& P, int b, int h, int qt, int lane, XShared& sh,
+                                          const bf16* lk, const bf16* lv) {
+  constexpr int KT = XKW / 16, KS = XKW / 32;
   const int G = lane >> 4, col = lane & 15;
   const int Lq = P.chunk, Lk = P.lk, ldvt = P.ldvt;
-  const int k0 = kq * XKW;
-  const int nkt = min(KT, max(0, (Lk - k0 + 15) / 16));  // key tiles with keys (uniform)
-  if (!kv_staged) attn_unit_kv(P, unit, st);
-  attn_stage_q(P, b, h, sh.a.q);
-  // every wave's DMA landed, then the staged rows are visible to all
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt(wc_vm(0));
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  const bf16* lk = st;
-  const bf16* lv = st + kAttnVt;
-  int qt[XQT], qc[XQT];
+  const int nkt = (Lk + 15) / 16;  // <= KT (uniform)
+  const int r = qt * 16 + col, qc = min(r, Lq - 1);
+  bf16x8 qf[2];
 #pragma unroll
-  for (int t = 0; t < XQT; ++t) {
-    qt[t] = qg * XQT + t;
-    qc[t] = min(qt[t] * 16 + col, Lq - 1);
-  }
-  bf16x8 qf[XQT][2];
-#pragma unroll
-  for (int t = 0; t < XQT; ++t)
-#pragma unroll
-    for (int ds = 0; ds < 2; ++ds) {
-      const int r = qt[t] * 16 + col;
-      qf[t][ds] = *reinterpret_cast<const bf16x8*>(sh.a.q + r * 64 + rswz8(r, ds * 4 + G) * 8);
-    }
-  // S^T tiles: s[q][t] lane holds scores of keys k0 + 16 t + 4 G + i, query col
-  f32x4 s[XQT][KT];
+  for (int ds = 0; ds < 2; ++ds)
+    qf[ds] = *reinterpret_cast<const bf16x8*>(sh.a.q + r * 64 + rswz8(r, ds * 4 + G) * 8);
+  f32x4 s[KT];
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
-#pragma unroll
-    for (int q = 0; q < XQT; ++q) s[q][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (t >= nkt) continue;  // wave-uniform
-    const int key = k0 + t * 16 + col;  // < 256: inside the staged rows
+    const int key = t * 16 + col;
 #pragma unroll
     for (int ds = 0; ds < 2; ++ds) {
       const bf16x8 kf = *reinterpret_cast<const bf16x8*>(lk + key * 64 + rswz8(key, ds * 4 + G) * 8);
-#pragma unroll
-      for (int q = 0; q < XQT; ++q)
-        s[q][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[q][ds], s[q][t], 0, 0, 0);
+      s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ds], s[t], 0, 0, 0);
     }
   }
-  // exact softmax: maxima and sums of the key quarters meet in LDS (keys
-  // past Lk, including rows never staged, are masked before any use)
+  float mx = -INFINITY;
 #pragma unroll
-  for (int q = 0; q < XQT; ++q) {
-    float mx = -INFINITY;
+  for (int t = 0; t < KT; ++t)
 #pragma unroll
-    for (int t = 0; t < KT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = k0 + t * 16 + 4 * G + i;
-        const bool vis = key < Lk && !(P.causal && key > qc[q]);
-        s[q][t][i] = vis ? s[q][t][i] * P.scale : -INFINITY;
-        mx = fmaxf(mx, s[q][t][i]);
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    if (lane < 16) sh.a.amax[kq][qt[q]][lane] = mx;
-  }
-  wg_sync_lds();
+    for (int i = 0; i < 4; ++i) {
+      const int key = t * 16 + 4 * G + i;
+      const bool vis = key < Lk && !(P.causal && key > qc);
+      s[t][i] = vis ? s[t][i] * P.scale : -INFINITY;
+      mx = fmaxf(mx, s[t][i]);
+    }
+  mx = xor32_max(xor16_max(mx));
   constexpr float kLog2e = 1.4426950408889634f;
+  float sum = 0.f;
 #pragma unroll
-  for (int q = 0; q < XQT; ++q) {
-    float m = sh.a.amax[0][qt[q]][col];
+  for (int t = 0; t < KT; ++t)
 #pragma unroll
-    for (int j = 1; j < XKQ; ++j) m = fmaxf(m, sh.a.amax[j][qt[q]][col]);
-    float sum = 0.f;
+    for (int i = 0; i < 4; ++i) {
+      const float ev = s[t][i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((s[t][i] - mx) * kLog2e);
+      s[t][i] = ev;
+      sum += ev;
+    }
+  sum = xor32_sum(xor16_sum(sum));
+  const float rl = 1.0f / sum;  // one division per query; P = e * (1 / l)
+  f32x4 o[4];
 #pragma unroll
-    for (int t = 0; t < KT; ++t)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float ev =
-            s[q][t][i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((s[q][t][i] - m) * kLog2e);
-        s[q][t][i] = ev;
-        sum += ev;
-      }
-    sum += __shfl_xor(sum, 16, 64);
-    sum += __shfl_xor(sum, 32, 64);
-    if (lane < 16) sh.a.asum[kq][qt[q]][lane] = sum;
-  }
-  wg_sync_lds();
-  // O^T = V^T . P^T over 32-key steps; contraction index 8 G + j <-> key
-  // 32 ks + 16 (j / 4) + 4 G + j % 4 (both operands)
-  f32x4 o[XQT][4];
-#pragma unroll
-  for (int q = 0; q < XQT; ++q)
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[q][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float inv[XQT];
-#pragma unroll
-  for (int q = 0; q < XQT; ++q) {
-    float l = sh.a.asum[0][qt[q]][col];
-#pragma unroll
-    for (int j = 1; j < XKQ; ++j) l += sh.a.asum[j][qt[q]][col];
-    inv[q] = l;
-  }
+  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     if (2 * ks >= nkt) continue;  // wave-uniform
-    const int kk = k0 + 32 * ks + 4 * G;  // < ldvt here
-    bf16x8 pf[XQT];
+    const int kk = 32 * ks + 4 * G;
+    bf16x8 pf;
 #pragma unroll
-    for (int q = 0; q < XQT; ++q)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        pf[q][i] = f2bf(s[q][2 * ks][i] / inv[q]);
-        pf[q][4 + i] = f2bf(s[q][2 * ks + 1][i] / inv[q]);
-      }
+    for (int i = 0; i < 4; ++i) {
+      pf[i] = f2bf(s[2 * ks][i] * rl);
+      pf[4 + i] = f2bf(s[2 * ks + 1][i] * rl);
+    }
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
       const int d = dt * 16 + col;
@@ -762,41 +725,147 @@ __device__ void attn_unit(CPhase& P, int unit, XShared& sh, bf16* st, bool kv_st
       const uint64_t hi =
           *reinterpret_cast<const uint64_t*>(row + vswz(d, (kk + 16) >> 3, ldvt) * 8 + (kk & 7));
       const u32x4 w4 = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
-#pragma unroll
-      for (int q = 0; q < XQT; ++q)
-        o[q][dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w4), pf[q],
-                                                           o[q][dt], 0, 0, 0);
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w4), pf, o[dt], 0, 0, 0);
     }
   }
-  // partial O^T of this key quarter: lane holds O^T[dt*16 + 4G + i][col]
+  if (r >= Lq) return;
+  const int om = b * P.chunk + r;  // row of the fragment-major output
 #pragma unroll
-  for (int q = 0; q < XQT; ++q)
+  for (int dt = 0; dt < 4; ++dt) {
+    float v[4];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int i = 0; i < 4; ++i) v[i] = o[dt][i];
+    st4_wt(P.o + frag_off(om, h * 64 + dt * 16 + 4 * G), v);
+  }
+}
+
+// kv_staged: this unit's K and V^T DMA was issued already
+__device__ void attn_unit(CPhase& P, int unit, XShared& sh, bf16* st, bool kv_staged) {
+  int lane = threadIdx.x & 63;
+  // opaque: lane-derived constants are recomputed here, not hoisted out of
+  // the phase loop (where they would only be spilled)
+  asm volatile("" : "+v"(lane));
+  const int wave = wave_id();
+  int b, h, qt;
+  attn_decode(P, unit, b, h, qt);
+  const int G = lane >> 4, col = lane & 15;
+  const int Lq = P.chunk, Lk = P.lk, ldvt = P.ldvt;
+  const bool solo = Lk <= XKW;  // uniform
+  if (!kv_staged) attn_unit_kv(P, unit, st);
+  if (solo) attn_stage_q(P, b, h, 0, 8, sh.a.q);
+  else attn_stage_q(P, b, h, qt * 16, 2, sh.a.q);
+  // every wave's DMA landed, then the staged rows are visible to all
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(wc_vm(0));
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  const bf16* lk = st;
+  const bf16* lv = st + kAttnVt;
+  if (solo) {
+    if (wave < 4) attn_solo(P, b, h, wave, lane, sh, lk, lv);
+    return;
+  }
+  // this wave's 32 keys against the unit's query tile
+  constexpr int KT = XKG / 16;  // 2 key tiles, one 32-key step
+  const int k0 = wave * XKG;
+  const int nkt = min(KT, max(0, (Lk - k0 + 15) / 16));  // key tiles with keys (uniform)
+  const int qc = min(qt * 16 + col, Lq - 1);
+  bf16x8 qf[2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) sh.a.o[kq][qt[q]][dt * 16 + 4 * G + i][col] = o[q][dt][i];
-  wg_sync_lds();
-  // the waves of key quarter 0 sum the quarters in order and store
-  if (kq == 0) {
+  for (int ds = 0; ds < 2; ++ds)
+    qf[ds] = *reinterpret_cast<const bf16x8*>(sh.a.q + col * 64 + rswz8(col, ds * 4 + G) * 8);
+  // S^T tiles: s[t] lane holds scores of keys k0 + 16 t + 4 G + i, query col
+  f32x4 s[KT];
 #pragma unroll
-    for (int q = 0; q < XQT; ++q) {
-      const int qi = qt[q] * 16 + col;
-      if (qi >= Lq) continue;
-      const int om = b * P.chunk + qi;  // row of the fragment-major output
+  for (int t = 0; t < KT; ++t) {
+    s[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (t >= nkt) continue;  // wave-uniform
+    const int key = k0 + t * 16 + col;  // < XMAXK: inside the staged rows
 #pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        float r[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d = dt * 16 + 4 * G + i;
-          float t = sh.a.o[0][qt[q]][d][col];
-#pragma unroll
-          for (int j = 1; j < XKQ; ++j) t += sh.a.o[j][qt[q]][d][col];
-          r[i] = t;
-        }
-        st4_wt(P.o + frag_off(om, h * 64 + dt * 16 + 4 * G), r);
-      }
+    for (int ds = 0; ds < 2; ++ds) {
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(lk + key * 64 + rswz8(key, ds * 4 + G) * 8);
+      s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ds], s[t], 0, 0, 0);
     }
+  }
+  // exact softmax: the key groups' maxima and sums meet in LDS (keys past
+  // Lk, including rows never staged, are masked before any use)
+  float mx = -INFINITY;
+#pragma unroll
+  for (int t = 0; t < KT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = k0 + t * 16 + 4 * G + i;
+      const bool vis = key < Lk && !(P.causal && key > qc);
+      s[t][i] = vis ? s[t][i] * P.scale : -INFINITY;
+      mx = fmaxf(mx, s[t][i]);
+    }
+  mx = xor32_max(xor16_max(mx));
+  if (lane < 16) sh.a.amax[wave][lane] = mx;
+  wg_sync_lds();
+  float m = sh.a.amax[0][col];
+#pragma unroll
+  for (int j = 1; j < XW; ++j) m = fmaxf(m, sh.a.amax[j][col]);
+  constexpr float kLog2e = 1.4426950408889634f;
+  float sum = 0.f;
+#pragma unroll
+  for (int t = 0; t < KT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ev = s[t][i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((s[t][i] - m) * kLog2e);
+      s[t][i] = ev;
+      sum += ev;
+    }
+  sum = xor32_sum(xor16_sum(sum));
+  if (lane < 16) sh.a.asum[wave][lane] = sum;
+  wg_sync_lds();
+  float l = sh.a.asum[0][col];
+#pragma unroll
+  for (int j = 1; j < XW; ++j) l += sh.a.asum[j][col];
+  const float rl = 1.0f / l;  // one division per query; P = e * (1 / l)
+  // O^T = V^T . P^T over the wave's 32 keys; contraction index 8 G + j <->
+  // key k0 + 16 (j / 4) + 4 G + j % 4 (both operands)
+  f32x4 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (nkt > 0) {  // wave-uniform
+    bf16x8 pf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      pf[i] = f2bf(s[0][i] * rl);
+      pf[4 + i] = f2bf(s[1][i] * rl);
+    }
+    const int kk = k0 + 4 * G;  // < ldvt here
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int d = dt * 16 + col;
+      const bf16* row = lv + d * ldvt;
+      const uint64_t lo = *reinterpret_cast<const uint64_t*>(row + vswz(d, kk >> 3, ldvt) * 8 + (kk & 7));
+      const uint64_t hi =
+          *reinterpret_cast<const uint64_t*>(row + vswz(d, (kk + 16) >> 3, ldvt) * 8 + (kk & 7));
+      const u32x4 w4 = {(uint32_t)lo, (uint32_t)(lo >> 32), (uint32_t)hi, (uint32_t)(hi >> 32)};
+      o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w4), pf, o[dt], 0, 0, 0);
+    }
+  }
+  // partial O^T of this key group: lane holds O^T[dt*16 + 4G + i][col]
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sh.a.o[wave][dt * 16 + 4 * G + i][col] = o[dt][i];
+  wg_sync_lds();
+  // wave dt < 4 sums d-tile dt over the key groups in order and stores it
+  const int qi = qt * 16 + col;
+  if (wave < 4 && qi < Lq) {
+    const int dt = wave;
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int d = dt * 16 + 4 * G + i;
+      float t = sh.a.o[0][d][col];
+#pragma unroll
+      for (int j = 1; j < XW; ++j) t += sh.a.o[j][d][col];
+      r[i] = t;
+    }
+    st4_wt(P.o + frag_off(b * P.chunk + qi, h * 64 + dt * 16 + 4 * G), r);  // fragment-major
   }
 }
 
@@ -847,15 +916,6 @@ __device__ __forceinline__ unsigned touch_phase(CPhase* ph) {
   return t;
 }
 
-// header fields of a phase used before its wait (read one phase ahead)
-struct Hdr {
-  int kind, epi, units, col_tiles, N, K, ldw;
-  const bf16* w;
-};
-__device__ __forceinline__ Hdr read_hdr(CPhase& P) {
-  return Hdr{P.kind, P.epi, P.units, P.col_tiles, P.N, P.K, P.ldw, P.w};
-}
-
 __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
   __shared__ XShared sh;
   __shared__ __attribute__((aligned(1024))) bf16 s_w[XW][XKS * XWSTEP];  // per-wave weights
@@ -899,27 +959,29 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
     if (s_rank < 0) return;
   }
 
-  Hdr h = read_hdr(g.ph[0]);
+  if (wave == 1) {
+    const unsigned t = touch_phase(g.ph) ^ (g.n_ph > 1 ? touch_phase(g.ph + 1) : 0u);
+    asm volatile("" ::"s"(t));
+  }
   for (int p = 0; p < g.n_ph; ++p) {
-    const Hdr cur = h;
-    if (p + 1 < g.n_ph) h = read_hdr(g.ph[p + 1]);  // next phase's header, early
-    if (rank >= cur.units) continue;
     CPhase& P = g.ph[p];
-    const int mine = (cur.units - rank + team - 1) / team;
+    if (rank >= P.units) continue;
+    const int mine = (P.units - rank + team - 1) / team;
     GemmRegs r;
     bf16* sw = s_w[wave];
     // weights of the first unit (and the K / V^T of a cross-attention unit)
     // before the wait: they do not depend on it
-    if (cur.kind == XK_GEMM) {
-      dma_w(cur.epi, cur.w, cur.N, cur.K, cur.ldw, rank % cur.col_tiles, sw);
-      if (P.norm_w) dma_gain(P.norm_w, cur.K, sh.g.gain[wave]);
+    if (P.kind == XK_GEMM) {
+      dma_w(P.epi, P.w, P.N, P.K, P.ldw, rank % P.col_tiles, sw);
+      if (P.norm_w) dma_gain(P.norm_w, P.K, sh.g.gain[wave]);
     }
-    else if (cur.kind == XK_ATTN && P.kv_static)
+    else if (P.kind == XK_ATTN && P.kv_static)
       attn_unit_kv(P, rank, &s_w[0][0]);
     if (p > 0) {
-      if (wave == 1) {
-        // while wave 0 waits: this phase's table entry into the scalar cache
-        const unsigned t = touch_phase(g.ph + p);
+      if (wave == 1 && p + 1 < g.n_ph) {
+        // while wave 0 waits: the next phase's table entry into the scalar
+        // cache (this one's was touched a phase ago)
+        const unsigned t = touch_phase(g.ph + p + 1);
         asm volatile("" ::"s"(t));
       }
       if (wave == 0) {
@@ -929,10 +991,10 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
       __syncthreads();
       if (s_rank < 0) return;
     }
-    if (cur.kind == XK_GEMM) {
+    if (P.kind == XK_GEMM) {
       for (int j = 0; j < mine; ++j) {
         const int u = rank + j * team;
-        const int ct = u % cur.col_tiles, grp = u / cur.col_tiles;
+        const int ct = u % P.col_tiles, grp = u / P.col_tiles;
         const int t0 = grp * P.group_tiles, t1 = min(t0 + P.group_tiles, 4);
         const bool vt = vt_unit(P, ct);
         const EpiItem it = epi_item(P, ct, t0, t1);
@@ -941,14 +1003,13 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
         // one row group: the activations stay in registers for the phase's units
         const bool load = j == 0 || P.row_groups > 1;
         if (load) {
-          load_x(P, r, sh.g.gain[wave], t0, t1);
+          load_x(P, r, t0, t1);
           if (P.norm_w) {
             // per-row sums of squares of the whole K range meet in LDS
 #pragma unroll
             for (int tm = 0; tm < 4; ++tm) {
               float t = r.ss[tm];
-              t += __shfl_xor(t, 16, 64);
-              t += __shfl_xor(t, 32, 64);
+              t = xor32_sum(xor16_sum(t));
               if (lane < 16) sh.g.ss[wave][tm * 16 + lane] = t;
             }
           }
@@ -960,12 +1021,12 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(wc_vm(0));
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        gemm_mma(P, r, sw, acc, t0, t1);
+        gemm_mma(P, r, sw, P.norm_w ? sh.g.gain[wave] : nullptr, acc, t0, t1);
         put_partial(acc, sh);
         wg_sync_lds();  // also: this wave's weight reads are done
         // the next unit's weights stream in during this unit's epilogue
         if (j + 1 < mine)
-          dma_w(cur.epi, cur.w, cur.N, cur.K, cur.ldw, (u + team) % cur.col_tiles, sw);
+          dma_w(P.epi, P.w, P.N, P.K, P.ldw, (u + team) % P.col_tiles, sw);
         if (load && P.norm_w) {
           if (tid < XBM) {
             float t = 0.f;
@@ -979,7 +1040,7 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
         else gemm_epilogue(P, it, e, sh);
         wg_sync_lds();  // partial tiles free for the next unit
       }
-    } else if (cur.kind == XK_ATTN) {
+    } else if (P.kind == XK_ATTN) {
       for (int j = 0; j < mine; ++j) {
         attn_unit(P, rank + j * team, sh, &s_w[0][0], j == 0 && P.kv_static);
         wg_sync_lds();  // LDS free for the next unit
@@ -1139,7 +1200,10 @@ size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, La
       XPhase T{};
       T.kind = XK_ATTN;
       T.M = M;
-      T.units = d->batch * d->n_q_heads;
+      // one unit per (sample, head) when one wave takes every key, else per
+      // (sample, head, 16-query tile)
+      T.q_tiles = (Ly.cross ? d->prefix_len : d->chunk) <= XKW ? 1 : (d->chunk + 15) / 16;
+      T.units = d->batch * d->n_q_heads * T.q_tiles;
       T.heads = d->n_q_heads; T.kv_heads = d->n_kv_heads;
       T.chunk = d->chunk;
       T.scale = 0.125f;

@@ -729,8 +729,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
       float t = ssq[tm];
-      t += __shfl_xor(t, 16, 64);
-      t += __shfl_xor(t, 32, 64);
+      t = xor32_sum(xor16_sum(t));
       rs[tm] = 1.0f / sqrtf(t / (float)p.K + p.norm_eps);
     }
   }
@@ -1354,8 +1353,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
 #pragma unroll
     for (int tm = 0; tm < TM; ++tm) {
       float t = ss[tm];
-      t += __shfl_xor(t, 16, 64);
-      t += __shfl_xor(t, 32, 64);
+      t = xor32_sum(xor16_sum(t));
       if (lane < 16) s_ss[wave][tm * 16 + lane] = t;
     }
   }

@@ -29,15 +29,39 @@ __device__ __forceinline__ bf16 f2bf(float x) { return (bf16)x; }
 // round an fp32 value through bf16 (models a bf16 tensor boundary in torch)
 __device__ __forceinline__ float rbf(float x) { return (float)(bf16)x; }
 
+// A value combined with the one of lane l ^ 16 (l ^ 32) of the wave:
+// v_permlane16_swap / v_permlane32_swap with both operands the value return
+// it and its partner in the two results (a VALU exchange, where a shuffle
+// would be an LDS permute).  Sums and maxima are commutative, so the result
+// equals v + partner bit for bit.
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
+  v = xor16_sum(xor32_sum(v));
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, SVLA_WAVE);
+  for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, SVLA_WAVE);
   return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
+  v = xor16_max(xor32_max(v));
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, SVLA_WAVE));
+  for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, SVLA_WAVE));
   return v;
 }
 
