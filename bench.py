@@ -10,9 +10,14 @@ replay).
 Prints ONE JSON line:
   value        chunks/s at batch 32 (whole job; higher is better)
   latency      ms per chunk at batch 1 (median of >= 50 chunks)
-  roofline     the dominant kernel (ViT MLP up-projection GEMM, bf16 MFMA):
-               algorithmic FLOPs / average launch time from HIP events on its
-               stream, against the 2.5 PFLOP/s dense bf16 peak
+  latency_bs1  ms per chunk at batch 1, with its roofline: the chunk's floor
+               = max(FLOPs / MFMA peak, bytes / HBM peak) (every weight once,
+               the expert's re-read per Euler step) against the median time
+  roofline     the dominant kernel -- the (entry point, shape, epilogue) group
+               with the most time per batch-32 chunk in a live census of one
+               chunk (smolvla.census): algorithmic FLOPs (or bytes) / average
+               launch time from HIP events on its stream, against the 2.5 PFLOP/s
+               dense bf16 (or 8 TB/s HBM) peak
   cpu_baseline the CPU oracle (PyTorch bf16 restatement of the reference
                modules) timed on this host's cores on a bounded sample
 """
@@ -98,50 +103,38 @@ def _up_proj_launcher(cfg, M, x, w_packed, bias, wide):
     return lambda: ops.linear(x, w_packed, bias=bias, act="gelu_" + v.gelu, out=out)
 
 
-def dominant_kernel_roofline(eng, iters):
-    """The ViT MLP up-projection (GEMM 96k x 3072 x 768 at batch 32 with the
-    bias + tanh-GELU epilogue; the only GEMM instantiated with GELU), launched
-    as the engine launches it, `iters` times back-to-back on the current
-    stream between two HIP events."""
-    from smolvla import layers
-    cfg = eng.cfg
-    v = cfg.vit
-    P = eng.vit[0]
-    M = eng.vit_x.shape[0]
-    x = eng.vbufs.get("vh", M, v.hidden)
-    wide = layers.vit_wide_ok(v, M)
-    run = _up_proj_launcher(cfg, M, x, P["wup"], P["bup"], wide)
-    for _ in range(3):
-        run()
-    torch.cuda.synchronize()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record()
-    for _ in range(iters):
-        run()
-    b.record()
-    b.synchronize()
-    avg_ms = a.elapsed_time(b) / iters
-    flops = 2.0 * M * v.inter * v.hidden
-    achieved = flops / (avg_ms * 1e-3) / 1e12
-    hbm_bytes = 2.0 * (M * v.hidden + v.inter * v.hidden + M * v.inter + v.inter)
+def census_groups(eng):
+    """Group and time every libsvla call of one eager chunk of ``eng``."""
+    from smolvla import census
+    was = eng.use_graph
+    eng.use_graph = False
+    try:
+        census.record_chunk(eng)           # warm-up
+        calls = census.record_chunk(eng)
+    finally:
+        eng.use_graph = was
+    groups = census.group_calls(calls, eng.cfg, eng.B)
+    return census.time_groups(groups)
+
+
+def dominant_roofline(eng):
+    """Roofline line of the group with the most time per chunk."""
+    from smolvla import census
+    groups = census_groups(eng)
+    top = max(groups, key=lambda g: g.us * g.n)
+    ach, frac, unit = top.row()
+    total_us = sum(g.us * g.n for g in groups)
+    rec = {"kernel": f"{top.name}: {top.label}", "launches_per_chunk": top.n,
+           "share_of_chunk": round(top.us * top.n / total_us, 4),
+           "bound": top.bound, "achieved": round(ach, 1),
+           "peak": PEAK_BF16_TFLOPS if top.bound == "mfma" else PEAK_HBM_GBS, "unit": unit,
+           "frac": round(frac, 4), "avg_launch_us": round(top.us, 2),
+           "algorithmic_flops": top.flops, "algorithmic_bytes": top.bytes, "traffic": None}
     tr = load_traffic()
-    traffic = tr.get("bytes_per_launch") if tr and tr.get("shape") == [M, v.inter, v.hidden] else None
-    from smolvla import _lib
-    tile = _lib.load().svla_gemm_tile_choice(M, v.inter, v.hidden, 1)
-    kname = {8: "gemm_wide_kernel<0, false, 0, 1, false> (persistent 256x256 tile, 5-stage "
-                "LDS-DMA ring, LDS-staged bias + tanh-GELU epilogue, streaming stores" +
-                (", slab-blocked activations, weights and output)" if wide else ")"),
-             7: "gemm_pipe_kernel<128, 128, 0, false, 0, 1> (128x128 LDS-DMA pipeline, "
-                "bias + tanh-GELU epilogue)"}.get(tile, f"GEMM tile configuration {tile}")
-    return {
-        "kernel": kname + ": ViT MLP up-projection",
-        "shape": [M, v.inter, v.hidden],
-        "bound": "mfma", "achieved": round(achieved, 1), "peak": PEAK_BF16_TFLOPS,
-        "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-        "avg_launch_us": round(avg_ms * 1e3, 2), "algorithmic_bytes": hbm_bytes,
-        "traffic": traffic,
-    }
+    m = top.label.split()[1] if top.label.startswith(("linear", "linear_wide")) else None
+    if tr and m and "x".join(map(str, tr.get("shape", []))) == m:
+        rec["traffic"] = tr.get("bytes_per_launch")
+    return rec, groups
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "dominant_kernel_traffic.json"
@@ -228,6 +221,38 @@ def traffic_summary(fetch_csv, write_csv, shape):
     print(json.dumps(rec))
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def chunk_floor(cfg, params, batch=1):
+    """(floor_us, bound, flops, bytes) of one chunk: max of FLOPs at the MFMA
+    peak and bytes at the HBM peak, bytes = every weight once + the expert
+    weights re-read by each later Euler step."""
+    from smolvla import census
+    flops = chunk_flops(cfg, batch)
+    w = 0
+    stack = [params]
+    while stack:
+        x = stack.pop()
+        if isinstance(x, dict):
+            stack.extend(x.values())
+        elif isinstance(x, (list, tuple)):
+            stack.extend(x)
+        elif torch.is_tensor(x):
+            w += x.numel() * x.element_size()
+    by = w + (cfg.num_steps - 1) * census.expert_step_weight_bytes(cfg)
+    t_mfma = flops / (PEAK_BF16_TFLOPS * 1e12) * 1e6
+    t_hbm = by / (PEAK_HBM_GBS * 1e9) * 1e6
+    return (max(t_mfma, t_hbm), "mfma" if t_mfma >= t_hbm else "hbm", flops, by)
+
+
 def cpu_baseline(cfg, params, seconds):
     """CPU oracle (PyTorch bf16 restatement of the reference modules) on this
     host: bs=1 chunks until `seconds` of work (after one warm-up chunk)."""
@@ -245,10 +270,41 @@ def cpu_baseline(cfg, params, seconds):
             if el >= seconds or n >= 50:
                 break
     return {"value": round(n / el, 4), "unit": "chunks/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "kind": "port", "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
             "sample": f"{n} full bs=1 chunks (3x512^2 cameras, 241-token prefix, 10 Euler "
                       f"steps) in {el:.1f} s, torch {torch.__version__} bf16 on CPU",
             "ms_per_chunk": round(el / n * 1e3, 1)}
+
+
+def write_kernel_table(cfg, params, batch):
+    """profiles/kernel_table_bs<batch>.md: the census table of one chunk."""
+    from smolvla import census
+    from smolvla.params import smolvla_inputs
+    from smolvla.pipeline import SmolVLAEngine
+    eng = SmolVLAEngine(cfg, params, batch=batch)
+    eng.load_inputs(*smolvla_inputs(cfg, batch, seed=1, device="cuda"))
+    eng.capture()
+    for _ in range(3):
+        eng.step()
+    ts = time_chunks(eng, 10)
+    groups = census_groups(eng)
+    rows, total_ms = census.table(groups)
+    n_launch = sum(g.n for g in groups)
+    path = ROOT / "profiles" / f"kernel_table_bs{batch}.md"
+    path.write_text(
+        f"# Per-kernel census: one SmolVLA chunk at batch {batch}\n\n"
+        f"Command (repo root on the MI355X box): `python bench.py --kernel-table {batch}`\n\n"
+        f"Every libsvla call of one eager chunk, grouped by entry point, shape and epilogue; a group's "
+        f"calls are replayed in chunk order inside one HIP graph and timed with HIP events "
+        f"(median of 3 replays / launches).  Work per launch as `smolvla/census.py` states it "
+        f"(GEMM 2MNK FLOPs, attention 4 Sq Sk d per head, dense; bandwidth kernels bytes read + "
+        f"written; the fused expert its Euler steps' FLOPs and streamed weights); fraction of the "
+        f"2.5 PFLOP/s bf16 MFMA or 8 TB/s HBM peak.\n\n"
+        f"{n_launch} launches in {len(groups)} groups; sum of group times {total_ms:.3f} ms per "
+        f"chunk; the captured chunk replays in {statistics.median(ts):.3f} ms (median of 10).  "
+        f"Top 25 by time per chunk:\n\n{rows}\n")
+    log(f"wrote {path}: {n_launch} launches, {total_ms:.3f} ms summed, "
+        f"{statistics.median(ts):.3f} ms per graph replay")
 
 
 def main():
@@ -258,7 +314,6 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--batch", type=int, default=32)
     ap.add_argument("--latency-chunks", type=int, default=50)
-    ap.add_argument("--kernel-iters", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-latency", action="store_true")
@@ -266,6 +321,9 @@ def main():
                     help="only launch the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn the two --traffic-probe counter CSVs into the committed record")
+    ap.add_argument("--kernel-table", type=int, metavar="BATCH",
+                    help="only write the per-kernel census table of one chunk at this batch "
+                         "to profiles/kernel_table_bs<BATCH>.md")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs on a single GPU "
@@ -288,6 +346,9 @@ def main():
         return
     log("generating seeded random-init bf16 weights")
     params = smolvla_params(cfg, seed=0)
+    if args.kernel_table:
+        write_kernel_table(cfg, params, args.kernel_table)
+        return
     B = args.batch
     log(f"preparing engine at batch {B}")
     eng = SmolVLAEngine(cfg, params, batch=B)
@@ -308,8 +369,9 @@ def main():
     flops = chunk_flops(cfg, B)
     log(f"batch {B}: {ms_step:.2f} ms/chunk-batch, {value:.1f} chunks/s, "
         f"{flops / (ms_step * 1e-3) / 1e12:.1f} TFLOP/s end to end")
-    roof = dominant_kernel_roofline(eng, args.kernel_iters)
-    log(f"dominant kernel: {roof['avg_launch_us']} us/launch, {roof['achieved']} TFLOP/s")
+    roof, _ = dominant_roofline(eng)
+    log(f"dominant kernel: {roof['kernel']}, {roof['avg_launch_us']} us/launch x "
+        f"{roof['launches_per_chunk']}, {roof['achieved']} {roof['unit']}")
     del eng
     torch.cuda.empty_cache()
 
@@ -321,10 +383,15 @@ def main():
         e1.capture()
         time_chunks(e1, 10)
         ts = time_chunks(e1, args.latency_chunks)
-        lat = {"ms_per_chunk_median": round(statistics.median(ts), 3),
+        med = statistics.median(ts)
+        floor_us, bound, fl, by = chunk_floor(cfg, params, 1)
+        lat = {"ms_per_chunk_median": round(med, 3),
                "ms_per_chunk_min": round(min(ts), 3), "chunks": len(ts), "batch": 1,
-               "tflops_end_to_end": round(chunk_flops(cfg, 1) / (statistics.median(ts) * 1e-3)
-                                          / 1e12, 1)}
+               "tflops_end_to_end": round(fl / (med * 1e-3) / 1e12, 1),
+               "roofline": {"bound": bound, "floor_us": round(floor_us, 1),
+                            "achieved_tflops": round(fl / (med * 1e-3) / 1e12, 1),
+                            "achieved_gbs": round(by / (med * 1e-3) / 1e9, 1),
+                            "flops": fl, "bytes": by, "frac": round(floor_us / (med * 1e3), 4)}}
         log(f"batch 1 latency: median {lat['ms_per_chunk_median']} ms")
         del e1
         torch.cuda.empty_cache()

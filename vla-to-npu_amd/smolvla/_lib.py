@@ -119,8 +119,19 @@ class SvlaError(RuntimeError):
     pass
 
 
+_OBSERVER = None
+
+
+def set_observer(fn):
+    """Install ``fn(name, args, run) -> rc`` around every ``call`` (``run()``
+    makes the call), or remove it with None.  Used by the kernel census."""
+    global _OBSERVER
+    _OBSERVER = fn
+
+
 def call(name: str, *args):
-    rc = getattr(load(), name)(*args)
+    f = getattr(load(), name)
+    rc = f(*args) if _OBSERVER is None else _OBSERVER(name, args, lambda: f(*args))
     if rc != 0:
         what = ("invalid argument (shape / alignment)" if rc == -22 else
                 "split needs more scratch than the static array holds" if rc == -28 else

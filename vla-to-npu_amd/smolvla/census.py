@@ -1,0 +1,257 @@
+"""Per-kernel census of one chunk: every ``libsvla`` call of an eager chunk
+with its algorithmic work (FLOPs for the MFMA contractions, HBM bytes for the
+rest), timed per launch, grouped by kernel and shape.
+
+How a call is timed: the calls of one group (same entry point, shape and
+epilogue) are replayed in chunk order inside one captured HIP graph -- so
+Python launch overhead never sits between them, and consecutive launches
+touch different layers' weights as they do in a chunk -- and the graph's
+replay time is divided by the number of launches.
+
+Short groups are repeated inside their graph (16 launches at least), so the
+graph's own launch cost does not land on a single kernel.
+
+Work model (the units of the roofline fractions): a GEMM is 2 M N K FLOPs
+and reads A and W once and writes C once (+ residual / bias / norm gains);
+attention is 4 Sq Sk head_dim FLOPs per (sample, head), causal or not (dense
+count, as the chunk's FLOP total); norms, casts and elementwise kernels are
+their bytes read + written; the fused expert is the FLOPs of its Euler steps
+and the weights it streams once per step.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import statistics
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+
+def _v(a):
+    """Python value of a recorded ctypes argument."""
+    return a.value if isinstance(a, (ctypes.c_void_p, ctypes.c_int, ctypes.c_long,
+                                     ctypes.c_float, ctypes.c_double)) else a
+
+
+def expert_step_flops(cfg, batch):
+    """FLOPs of one Euler step of the action expert (dense attention count)."""
+    d, e = cfg.decoder, cfg.expert
+    A, L = cfg.chunk, cfg.prefix_len
+    n_cross = sum(cfg.is_cross(i) for i in range(cfg.expert_layers))
+    common = 2 * A * e.hidden * e.q_dim + 3 * 2 * A * e.inter * e.hidden
+    self_l = common + 2 * A * 2 * e.kv_dim * e.hidden + 4 * A * A * e.n_q_heads * 64
+    cross_l = common + 4 * A * L * e.n_q_heads * 64
+    io = 2 * A * e.hidden * (cfg.action_dim + 2 * e.hidden) + 2 * A * cfg.action_dim * e.hidden
+    return batch * ((cfg.expert_layers - n_cross) * self_l + n_cross * cross_l + io)
+
+
+def expert_step_weight_bytes(cfg):
+    """bf16 weight bytes one Euler step streams (every projection once)."""
+    e = cfg.expert
+    H = e.hidden
+    total = 0
+    for i in range(cfg.expert_layers):
+        qkv = e.q_dim if cfg.is_cross(i) else e.q_dim + 2 * e.kv_dim
+        total += (qkv * H + e.q_dim * H + 2 * e.inter * H + e.inter * H) * 2
+    return total + (cfg.action_dim * H + 2 * H * H + H * cfg.action_dim) * 2
+
+
+def work(name, args, cfg, batch):
+    """(bound, flops, bytes, label) of one recorded call."""
+    a = [_v(x) for x in args]
+    if name in ("svla_linear_bf16", "svla_linear_scratch_bf16", "svla_linear_wide_bf16"):
+        m, n, k = a[10], a[11], a[12]
+        res, bias, out_f32 = a[6], a[4] or a[5], (a[15] if name != "svla_linear_wide_bf16" else 0)
+        norm = a[16] if name != "svla_linear_wide_bf16" else None
+        act = a[14]
+        by = 2 * (m * k + n * k) + (4 if out_f32 else 2) * m * n + (2 * m * n if res else 0)
+        by += (2 * k if norm else 0) + (2 * n if bias else 0)
+        tag = "".join([" norm" if norm else "", " bias" if bias else "", f" act{act}" if act else "",
+                       " +res" if res else "", " f32out" if out_f32 else ""])
+        kind = "linear_wide" if name == "svla_linear_wide_bf16" else "linear"
+        return "mfma", 2 * m * n * k, by, f"{kind} {m}x{n}x{k}{tag}"
+    if name == "svla_linear_rope_bf16":
+        m, n, k = a[6], a[7], a[8]
+        by = 2 * (m * k + n * k + m * n) + (2 * k if a[13] else 0)
+        return "mfma", 2 * m * n * k, by, f"linear+rope {m}x{n}x{k}{' norm' if a[13] else ''}"
+    if name == "svla_linear_silu_mul_bf16":
+        m, inter, k = a[6], a[7], a[8]
+        by = 2 * (m * k + 2 * inter * k + m * inter) + (2 * k if a[9] else 0)
+        return ("mfma", 2 * m * 2 * inter * k, by,
+                f"linear gate|up+silu*mul {m}x{2 * inter}x{k}{' norm' if a[9] else ''}")
+    if name == "svla_patch_embed_bf16":
+        n_img, ch, img, p, emb = a[6], a[7], a[8], a[9], a[10]
+        t = (img // p) ** 2
+        kk = ch * p * p
+        by = 2 * (n_img * ch * img * img + emb * kk + 2 * n_img * t * emb)
+        return "mfma", 2 * n_img * t * emb * kk, by, f"patch embed {n_img * t}x{emb}x{kk}"
+    if name == "svla_connector_bf16":
+        n_img, grid, hid, sc, n_out = a[5], a[6], a[7], a[8], a[9]
+        m, kk = n_img * (grid // sc) ** 2, hid * sc * sc
+        by = 2 * (n_img * grid * grid * hid + n_out * kk + m * n_out)
+        return "mfma", 2 * m * n_out * kk, by, f"connector {m}x{n_out}x{kk}"
+    if name == "svla_action_out_euler":
+        m, n, k = a[8], a[9], a[10]
+        by = 2 * (m * k + n * k) + 10 * m * n
+        return "mfma", 2 * m * n * k, by, f"action out+euler {m}x{n}x{k}"
+    if name == "svla_attention_bf16":
+        b, sq, sk, hq, hkv, hd, mask = a[12], a[13], a[14], a[15], a[16], a[17], a[19]
+        by = 2 * b * (2 * sq * hq * hd + 2 * sk * hkv * hd)
+        what = {0: "full", 1: "causal", 2: "prefix"}.get(mask, f"mask{mask}")
+        return ("mfma", 4 * b * hq * sq * sk * hd, by,
+                f"attention b{b} {sq}x{sk} {hq}/{hkv} heads {what}")
+    if name == "svla_expert_run":
+        steps = cfg.num_steps
+        by = steps * expert_step_weight_bytes(cfg)
+        return ("hbm", steps * expert_step_flops(cfg, batch), by,
+                f"fused action expert ({steps} Euler steps, batch {batch})")
+    if name == "svla_rmsnorm_bf16":
+        r, c = a[5], a[6]
+        return "hbm", 0, 2 * (2 * r * c + c), f"rmsnorm {r}x{c}"
+    if name == "svla_layernorm_bf16":
+        r, c = a[6], a[7]
+        return "hbm", 0, 2 * (2 * r * c + 2 * c), f"layernorm {r}x{c}"
+    if name == "svla_layernorm_blocked_bf16":
+        r, c = a[5], a[6]
+        return "hbm", 0, 2 * (2 * r * c + 2 * c), f"layernorm->blocked {r}x{c}"
+    if name == "svla_slab_block_bf16":
+        r, k = a[3], a[4]
+        return "hbm", 0, 4 * r * k, f"slab block {r}x{k}"
+    if name == "svla_embed_bf16":
+        hid, n_tok = a[3], a[8]
+        return "hbm", 0, 4 * n_tok * hid, f"token embed {n_tok}x{hid}"
+    if name == "svla_image_to_bf16":
+        n, h, w, out = a[2], a[3], a[4], a[6]
+        return "hbm", 0, n * h * w * 3 + 2 * n * 3 * out * out, f"image -> bf16 {n}x{h}x{w}"
+    if name == "svla_add_bf16":
+        return "hbm", 0, 6 * a[3], f"add {a[3]}"
+    if name in ("svla_silu_bf16", "svla_f32_to_bf16"):
+        return "hbm", 0, 4 * a[2], f"{name[5:]} {a[2]}"
+    if name == "svla_silu_mul_bf16":
+        return "hbm", 0, 6 * a[3], f"silu*mul {a[3]}"
+    if name == "svla_gelu_bf16":
+        return "hbm", 0, 4 * a[2], f"gelu {a[2]}"
+    return "hbm", 0, 0, name[5:]
+
+
+@dataclass
+class Group:
+    label: str
+    name: str
+    bound: str
+    flops: float
+    bytes: float
+    calls: list = field(default_factory=list)
+    us: float = 0.0          # per launch
+
+    @property
+    def n(self):
+        return len(self.calls)
+
+    def row(self):
+        per_s = self.us * 1e-6
+        if self.bound == "mfma":
+            ach = self.flops / per_s / 1e12
+            return ach, ach / PEAK_BF16_TFLOPS, "TFLOP/s"
+        ach = self.bytes / per_s / 1e9
+        return ach, ach / PEAK_HBM_GBS, "GB/s"
+
+
+# entry points that set state rather than launch work: not timed
+_SKIP = {"svla_init", "svla_version", "svla_gemm_set_tile", "svla_gemm_set_split",
+         "svla_gemm_tile_choice", "svla_expert_workspace_size", "svla_expert_prepare",
+         "svla_expert_status", "svla_time_embedding_bf16", "svla_rope_table"}
+
+
+def record_chunk(eng):
+    """The libsvla calls of one eager chunk of ``eng`` (a SmolVLAEngine with
+    ``use_graph=False``), in order."""
+    calls = []
+
+    def hook(name, args, run):
+        if name not in _SKIP:
+            calls.append((name, args))
+        return run()
+
+    _lib.set_observer(hook)
+    try:
+        eng.step()
+        torch.cuda.synchronize()
+    finally:
+        _lib.set_observer(None)
+    return calls
+
+
+def _launch(name, args):
+    """Launch a recorded call on the current stream."""
+    argv = list(args)
+    argv[-1] = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = getattr(_lib.load(), name)(*argv)
+    if rc != 0:
+        raise _lib.SvlaError(f"{name}: replay failed ({rc})")
+
+
+def group_calls(calls, cfg, batch):
+    groups = {}
+    for name, args in calls:
+        bound, fl, by, label = work(name, args, cfg, batch)
+        g = groups.get(label)
+        if g is None:
+            g = groups[label] = Group(label, name, bound, fl, by)
+        g.calls.append(args)
+    return list(groups.values())
+
+
+def time_groups(groups, reps=3):
+    """Per-launch time of every group (HIP-graph replay of its calls)."""
+    for g in groups:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for args in g.calls:        # warm-up, eager
+                _launch(g.name, args)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        # short groups repeat inside the graph: a graph launch costs ~20 us,
+        # which must not land on a single kernel
+        rounds = max(1, -(-16 // g.n))
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(rounds):
+                for args in g.calls:
+                    _launch(g.name, args)
+        graph.replay()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(reps):
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            graph.replay()
+            b.record()
+            b.synchronize()
+            ts.append(a.elapsed_time(b))
+        g.us = statistics.median(ts) * 1e3 / (g.n * rounds)
+        del graph
+    return groups
+
+
+def table(groups, top=25):
+    """Markdown rows of the ``top`` groups by time per chunk."""
+    total = sum(g.us * g.n for g in groups)
+    rows = ["| # | kernel (entry point: shape, epilogue) | launches | us / launch | "
+            "ms / chunk | % | work / launch | achieved | peak fraction |",
+            "|---:|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for i, g in enumerate(sorted(groups, key=lambda g: -g.us * g.n)[:top], 1):
+        ach, frac, unit = g.row()
+        wk = (f"{g.flops / 1e9:.3f} GFLOP" if g.bound == "mfma" else f"{g.bytes / 1e6:.3f} MB")
+        rows.append(f"| {i} | `{g.name}`: {g.label} | {g.n} | {g.us:.2f} | {g.us * g.n / 1e3:.3f} | "
+                    f"{100 * g.us * g.n / total:.1f} | {wk} | {ach:.1f} {unit} | "
+                    f"{frac:.3f} ({'MFMA' if g.bound == 'mfma' else 'HBM'}) |")
+    return "\n".join(rows), total / 1e3
