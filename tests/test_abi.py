@@ -53,10 +53,10 @@ def test_ops_refuse_cpu_tensors():
     (50, 720, 2048, 12),     # batch-1 expert down (split over workgroups)
     (241, 960, 960, 12),     # batch-1 prefix O
     (241, 960, 2560, 5),     # batch-1 prefix down: 32-column tile, split 2
-    (3072, 768, 3072, 7),    # batch-1 ViT down: 128x128 LDS-DMA pipeline
-    (3072, 3072, 768, 7),    # batch-1 ViT up
+    (3072, 768, 3072, 16),   # batch-1 ViT down: 64x64 line-DMA pipeline
+    (3072, 3072, 768, 14),   # batch-1 ViT up: 128x64 line-DMA pipeline
     (1600, 720, 960, 10),    # batch-32 expert O: 128x64 pipeline
-    (7712, 960, 2560, 1),    # batch-32 prefix down: register-staged 128x128
+    (7712, 960, 2560, 13),   # batch-32 prefix down: 128x128 line-DMA pipeline
     (98304, 3072, 768, 8),   # batch-32 ViT up: persistent 256x256 tile
 ])
 def test_gemm_tile_choice(m, n, k, tile):
@@ -92,4 +92,4 @@ def test_strict_forced_tile_without_kernel_is_einval(tile, norm, rope):
     finally:
         lib.svla_gemm_set_tile(-1)
     assert rc == -22
-    assert lib.svla_gemm_set_tile(13 | 0x100) == -22
+    assert lib.svla_gemm_set_tile(17 | 0x100) == -22

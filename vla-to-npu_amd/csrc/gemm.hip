@@ -525,6 +525,47 @@ constexpr int PBK = 32;
 
 __device__ __forceinline__ int pswz(int r, int g) { return g ^ ((r >> 1) & 3); }
 
+// Epilogue of the LDS-DMA pipelines (same lane layout as gemm_kernel with
+// MF = 16), one column tile at a time: all loads, then all stores.  rs: the
+// row scale 1 / rms of the lane's rows (NORM).
+template <int BM, int BN, int EPI, int ACT, bool NORM, int TN, int TM>
+__device__ __forceinline__ void pipe_epilogue(const GemmArgs& p, const f32x4 (&acc)[TN][TM],
+                                              const float (&rs)[TM], int m0, int n0, int wm,
+                                              int wn, int fr, int g) {
+  constexpr int WAVES_M = BM >= 128 ? 2 : 4, WAVES_N = 4 / WAVES_M;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr bool PAIRED = EPI == EPI_ROPE || EPI == EPI_SILU;
+  const int col_in = 4 * g;
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    // paired epilogues: the first half of each 64-column block pairs with the
+    // tile 32 columns on
+    if (PAIRED && (tn & 3) >= 2) continue;
+    const int n = n0 + wn * WN + tn * 16 + col_in;
+    int gm[TM], gn[TM];
+    EpiIn e[TM];
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      gm[tm] = min(m0 + wm * WM + tm * 16 + fr, p.M - 1);
+      gn[tm] = min(n, p.N - 4);
+    }
+    epi_load_groups<EPI, TM>(p, gm, gn, e);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      const int m = m0 + wm * WM + tm * 16 + fr;
+      if (m >= p.M || n >= p.N) continue;
+      float x1[4], x2[4];
+      const float sc = NORM ? p.alpha * rs[tm] : p.alpha;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x1[i] = acc[tn][tm][i] * sc;
+        x2[i] = PAIRED ? acc[(tn + 2) % TN][tm][i] * sc : 0.f;
+      }
+      epi_apply<EPI, ACT>(p, m, n, x1, x2, e[tm]);
+    }
+  }
+}
+
 template <int BM, int BN, int AMODE, bool NORM, int EPI, int ACT>
 __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
   constexpr int WAVES_M = BM >= 128 ? 2 : 4, WAVES_N = 4 / WAVES_M;
@@ -734,38 +775,209 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
     }
   }
 
-  // ---- epilogue (same lane layout as gemm_kernel with MF = 16), one column
-  // tile at a time: all loads, then all stores
-  constexpr bool PAIRED = EPI == EPI_ROPE || EPI == EPI_SILU;
-  const int col_in = 4 * g;
+  pipe_epilogue<BM, BN, EPI, ACT, NORM>(p, acc, rs, m0, n0, wm, wn, fr, g);
+}
+
+// ---- line-DMA pipeline: 64-wide K stages fetched as whole cache lines ------
+// Same tiles, waves and epilogue as gemm_pipe_kernel, but each LDS stage holds
+// a 64-element K slice and every DMA instruction fetches 8 rows x 128 bytes
+// (8 lanes per row): whole cache lines.  A CU's L1 serves misses at a per-line
+// rate, so the 16-row x 64-byte instructions of the 32-wide stages (each line
+// half used per instruction) bring about half the bytes per second (measured
+// on MI355X: 200 KB per CU in 6.1 us as 16 x 64 B, 3.1 us as 8 x 128 B).  Two
+// stages (the same LDS as four 32-wide ones): the next stage streams in while
+// the current one is consumed as two 32-wide MFMA K steps.  Row r holds its 8
+// 16-byte chunks at slots chunk ^ ((r >> 1) & 7), so a fragment read of 16
+// rows (16 lanes, one chunk) spreads over the banks.
+constexpr int LBK = 64;
+__device__ __forceinline__ int lswz(int r, int c) { return c ^ ((r >> 1) & 7); }
+
+template <int BM, int BN, int AMODE, bool NORM, int EPI, int ACT>
+__global__ __launch_bounds__(256, 2) void gemm_line_kernel(GemmArgs p) {
+  constexpr int WAVES_M = BM >= 128 ? 2 : 4, WAVES_N = 4 / WAVES_M;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 16, TN = WN / 16;          // 16x16 MFMA tiles per wave
+  constexpr int A_DMA = BM / 32, B_DMA = BN / 32;    // 1 KB (8-row) DMA blocks per wave per stage
+  static_assert(TM >= 1 && TN >= 1 && A_DMA >= 1 && B_DMA >= 1, "tile shape");
+  static_assert((EPI != EPI_ROPE && EPI != EPI_SILU) || WN % 64 == 0,
+                "paired epilogues need 64-column wave tiles");
+  __shared__ __attribute__((aligned(1024))) bf16 sA0[BM * LBK], sA1[BM * LBK];
+  __shared__ __attribute__((aligned(1024))) bf16 sB0[BN * LBK], sB1[BN * LBK];
+  __shared__ __attribute__((aligned(16))) bf16 s_gain[NORM ? 2048 : 8];  // norm gain (K <= 2048)
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int gn = gridDim.x;
+  const int tile = xcd_remap(blockIdx.y * gn + blockIdx.x, gn * gridDim.y);
+  int tm_idx, tn_idx;
+  tile_coords(tile, gridDim.y, gn, tm_idx, tn_idx);
+  const int m0 = tm_idx * BM, n0 = tn_idx * BN;
+  const int nk = p.K / LBK;  // full 64-wide stages (>= 1, checked by the launcher)
+
+  if constexpr (NORM) {
+    for (int c = tid * 8; c < p.K; c += 256 * 8)
+      *reinterpret_cast<bf16x8*>(&s_gain[c]) = ld8(p.norm_w + c);
+    __syncthreads();
+  }
+
+  // per-lane DMA source rows (fixed across stages): block b covers rows
+  // 8b .. 8b+7, lane -> row 8b + lane/8, LDS slot lane%8
+  int a_row[A_DMA], a_chunk[A_DMA], b_row[B_DMA], b_chunk[B_DMA];
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn) {
-    // paired epilogues: the first half of each 64-column block pairs with the
-    // tile 32 columns on
-    if (PAIRED && (tn & 3) >= 2) continue;
-    const int n = n0 + wn * WN + tn * 16 + col_in;
-    int gm[TM], gn[TM];
-    EpiIn e[TM];
+  for (int j = 0; j < A_DMA; ++j) {
+    const int r = (wave * A_DMA + j) * 8 + (lane >> 3);
+    a_row[j] = min(m0 + r, p.M - 1);
+    a_chunk[j] = lswz(r, lane & 7);
+  }
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-      gm[tm] = min(m0 + wm * WM + tm * 16 + fr, p.M - 1);
-      gn[tm] = min(n, p.N - 4);
-    }
-    epi_load_groups<EPI, TM>(p, gm, gn, e);
+  for (int j = 0; j < B_DMA; ++j) {
+    const int r = (wave * B_DMA + j) * 8 + (lane >> 3);
+    b_row[j] = min(n0 + r, p.N - 1);
+    b_chunk[j] = lswz(r, lane & 7);
+  }
+
+  auto issue = [&](auto SI, int kt) __attribute__((always_inline)) {
+    constexpr int S = decltype(SI)::value;
+    bf16* sa = S == 0 ? sA0 : sA1;
+    bf16* sb = S == 0 ? sB0 : sB1;
+    kt = min(kt, nk - 1);  // past the end: reload the last stage (never read)
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-      const int m = m0 + wm * WM + tm * 16 + fr;
-      if (m >= p.M || n >= p.N) continue;
-      float x1[4], x2[4];
-      const float sc = NORM ? p.alpha * rs[tm] : p.alpha;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x1[i] = acc[tn][tm][i] * sc;
-        x2[i] = PAIRED ? acc[(tn + 2) % TN][tm][i] * sc : 0.f;
+    for (int j = 0; j < A_DMA; ++j) {
+      const int blk = wave * A_DMA + j;
+      const int k = kt * LBK + a_chunk[j] * 8;
+      const bf16* ga;
+      if constexpr (AMODE == A_DENSE) ga = p.a + (long)a_row[j] * p.lda + k;
+      else {
+        // gathers: load_a's address map
+        if constexpr (AMODE == A_PSHUF) {
+          const int s_ = p.g_scale, E = p.g_hidden, grid = p.g_grid, gs = grid / s_;
+          const int per = gs * gs, mm = a_row[j];
+          const int img = mm / per, i = mm - img * per, hp = i / gs, wp = i - hp * gs;
+          const int sE = s_ * E, t = k / sE, rem = k - t * sE, u = rem / E, c = rem - u * E;
+          ga = p.a + ((long)img * grid * grid + (long)(s_ * hp + t) * grid + s_ * wp + u) * E + c;
+        } else {
+          const int P = p.p_patch, H = p.p_img, G = H / P, per = G * G, mm = a_row[j];
+          const int img = mm / per, tkn = mm - img * per, pr = tkn / G, pc = tkn - pr * G;
+          const int P2 = P * P, ch = k / P2, r = k - ch * P2, ky = r / P, kx = r - ky * P;
+          ga = p.a + (((long)img * p.p_chans + ch) * H + pr * P + ky) * H + pc * P + kx;
+        }
       }
-      epi_apply<EPI, ACT>(p, m, n, x1, x2, e[tm]);
+      __builtin_amdgcn_global_load_lds((void*)ga, (lds_ptr_t)(sa + blk * 512), 16, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < B_DMA; ++j) {
+      const int blk = wave * B_DMA + j;
+      const bf16* gb = p.b + (long)b_row[j] * p.ldb + kt * LBK + b_chunk[j] * 8;
+      __builtin_amdgcn_global_load_lds((void*)gb, (lds_ptr_t)(sb + blk * 512), 16, 0, 0);
+    }
+  };
+
+  f32x4 acc[TN][TM];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int fr = lane & 15, g = lane >> 4;
+  // fused RMSNorm as in gemm_pipe_kernel: gain on the way in, row sums of
+  // squares from the same fragments, 1 / rms in the epilogue
+  float ssq[TM];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) ssq[tm] = 0.f;
+  auto normalise = [&](bf16x8 (&fx)[TM], int k) {
+    if constexpr (NORM) {
+      const bf16x8 gw = *reinterpret_cast<const bf16x8*>(&s_gain[k]);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float xv = bf2f(fx[tm][j]);
+          ssq[tm] = __builtin_fmaf(xv, xv, ssq[tm]);
+          fx[tm][j] = f2bf(__fmul_rn(xv, bf2f(gw[j])));
+        }
+    }
+  };
+  auto mma = [&](const bf16x8 (&fw)[TN], const bf16x8 (&fx)[TM]) {
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+        acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[tn], fx[tm], acc[tn][tm], 0, 0, 0);
+  };
+
+  // one stage = two 32-wide MFMA K steps (chunks 4h + g, h = 0, 1)
+  auto compute = [&](auto SI, int kt) __attribute__((always_inline)) {
+    constexpr int S = decltype(SI)::value;
+    const bf16* sa = S == 0 ? sA0 : sA1;
+    const bf16* sb = S == 0 ? sB0 : sB1;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bf16x8 fw[TN], fx[TM];
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const int r = wn * WN + tn * 16 + fr;
+        fw[tn] = *reinterpret_cast<const bf16x8*>(&sb[r * LBK + lswz(r, 4 * h + g) * 8]);
+      }
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) {
+        const int r = wm * WM + tm * 16 + fr;
+        fx[tm] = *reinterpret_cast<const bf16x8*>(&sa[r * LBK + lswz(r, 4 * h + g) * 8]);
+      }
+      normalise(fx, kt * LBK + h * 32 + g * 8);
+      mma(fw, fx);
+    }
+  };
+
+  // Before each barrier: s_waitcnt vmcnt(0) lgkmcnt(0): the stage computed
+  // next has landed (it is the only one in flight), and this wave's LDS reads
+  // of the stage computed before the barrier have completed, since the DMA
+  // issued right after the barrier refills that stage.  gfx9 encoding.
+  constexpr int kWait0 = 0x070;
+  auto sync_step = [&]() __attribute__((always_inline)) {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(kWait0);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+
+  issue(I0{}, 0);
+  for (int kt = 0; kt < nk; kt += 2) {
+    sync_step();
+    issue(I1{}, kt + 1);
+    compute(I0{}, kt);
+    sync_step();
+    issue(I0{}, kt + 2);
+    if (kt + 1 < nk) compute(I1{}, kt + 1);
+  }
+  // drain the trailing (never read) DMA before the workgroup can exit
+  __builtin_amdgcn_s_waitcnt(0);
+
+  // K tail (K % 64 = 8 .. 56): 32-wide steps from global memory, zero past K
+  for (int kb = nk * LBK; kb < p.K; kb += 32) {
+    const int k = kb + g * 8;
+    bf16x8 fw[TN], fx[TM];
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) {
+      const int n = n0 + wn * WN + tn * 16 + fr;
+      fw[tn] = (k < p.K && n < p.N) ? ld8(p.b + (long)n * p.ldb + k) : bf16x8{};
+    }
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) fx[tm] = load_a<AMODE>(p, m0 + wm * WM + tm * 16 + fr, k);
+    normalise(fx, min(k, p.K - 8));  // fx is zero past K whatever the gain
+    mma(fw, fx);
+  }
+  float rs[TM];  // row scale of row tm * 16 + fr (the lane's epilogue rows)
+  if constexpr (NORM) {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      float t = ssq[tm];
+      t = xor32_sum(xor16_sum(t));
+      rs[tm] = 1.0f / sqrtf(t / (float)p.K + p.norm_eps);
     }
   }
+  pipe_epilogue<BM, BN, EPI, ACT, NORM>(p, acc, rs, m0, n0, wm, wn, fr, g);
 }
 
 // ---- wide GEMM: 256 x 256 block tile, one workgroup per CU -------------------
@@ -1493,7 +1705,8 @@ __global__ __launch_bounds__(256) void slab_block_kernel(const bf16* __restrict_
 
 // ---- launch ---------------------------------------------------------------
 enum TileId { T256 = 0, T128 = 1, T64x128 = 2, T64 = 3, S64 = 4, S32 = 5, T128S = 6,
-              P128 = 7, W256 = 8, P64 = 9, P128x64 = 10, P64x128 = 11, S16 = 12, NUM_TILES = 13 };
+              P128 = 7, W256 = 8, P64 = 9, P128x64 = 10, P64x128 = 11, S16 = 12, L128 = 13,
+              L128x64 = 14, L64x128 = 15, L64 = 16, NUM_TILES = 17 };
 
 // Launches tile configuration t; SVLA_EINVAL for a tile / epilogue pair that
 // has no kernel (the 128x64 pipeline and the 32-column skinny tile have no
@@ -1548,6 +1761,21 @@ int launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
     case S16:
       hipLaunchKernelGGL((skinny_kernel<16, AMODE, NORM, EPI, ACT>), grid, dim3(SK_WAVES * 64), 0, s, p);
       break;
+    case L128:
+      hipLaunchKernelGGL((gemm_line_kernel<128, 128, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      break;
+    case L128x64:
+      if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
+        hipLaunchKernelGGL((gemm_line_kernel<128, 64, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      else
+        return SVLA_EINVAL;
+      break;
+    case L64x128:
+      hipLaunchKernelGGL((gemm_line_kernel<64, 128, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      break;
+    case L64:
+      hipLaunchKernelGGL((gemm_line_kernel<64, 64, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      break;
     case S32:
       if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
         hipLaunchKernelGGL((skinny_kernel<32, AMODE, NORM, EPI, ACT>), grid, dim3(SK_WAVES * 64), 0, s, p);
@@ -1588,6 +1816,10 @@ TileCfg tile_dims(TileId id) {
     case T64: return {T64, 64, 64};
     case S64: return {S64, 64, 64};
     case S16: return {S16, 64, 16};
+    case L128: return {L128, 128, 128};
+    case L128x64: return {L128x64, 128, 64};
+    case L64x128: return {L64x128, 64, 128};
+    case L64: return {L64, 64, 64};
     default: return {S32, 64, 32};
   }
 }
@@ -1607,6 +1839,10 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, b
     if (g_force_tile == P64 && !pipe_ok) return tile_dims(T64);
     if ((g_force_tile == P128x64 || g_force_tile == P64x128) && !pipe_ok) return tile_dims(T64);
     if (g_force_tile == P128x64 && paired) return tile_dims(P64);  // paired needs 64-wide wave tiles
+    const bool line_ok = K >= LBK;
+    if ((g_force_tile == L128 || g_force_tile == L64x128) && !line_ok) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
+    if ((g_force_tile == L64 || g_force_tile == L128x64) && !line_ok) return pipe_ok ? tile_dims(P64) : tile_dims(T64);
+    if (g_force_tile == L128x64 && paired) return tile_dims(L64);
     return tile_dims((TileId)g_force_tile);
   }
   if (M <= kSkinnyMaxM) {
@@ -1638,11 +1874,27 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, b
   // wide tile beats the 128x128 pipeline from K = 512 (K = 768 + GELU: 675 vs
   // 752 us; K = 3072: 1603 vs 2285 us) and loses below (K = 256: 465 vs 430)
   if (wide_ok && K >= 512 && tiles(WBM, WBN) >= 2 * kNumCU) return tile_dims(W256);
+  const bool line_ok = K >= LBK;
   // dense A from M = 4096 (the batch-32 prefix, 7712 rows), measured on
-  // MI355X: the register-staged 128x128 kernel beats the pipeline -- gate|up
-  // + SiLU 114.5 -> 104.3 us, down 60.9 -> 57.7, QKV + RoPE 53.4 -> 52.1, O
-  // 31.5 -> 30.3; the gathers (patch embedding, connector) keep the pipeline
-  if (dense && M >= 4096) return tile_dims(T128);
+  // MI355X: the line-DMA pipeline beats the register-staged 128x128 kernel
+  // (itself ahead of the 32-wide pipeline) -- down 7712x960x2560 60.7 ->
+  // 47.9 us and O 7712x960x960 28.8 -> 25.0 on 128x128 line tiles, norm +
+  // QKV + RoPE 7712x1600x960 54.3 -> 49.4 on 64x128; norm + gate|up + SiLU
+  // 7712x5120x960 stays on the register-staged tile (121.5 vs 121.9 us); the
+  // gathers (patch embedding, connector) keep the pipeline
+  if (dense && M >= 4096) {
+    if (!line_ok || epi == EPI_SILU) return tile_dims(T128);
+    return tile_dims(paired ? L64x128 : L128);
+  }
+  // from M = 3072 (the batch-1 ViT, 3 images), measured on MI355X, line-DMA
+  // tiles: up 3072x3072x768 + GELU 38.0 -> 27.8 us (128x64), QKV
+  // 3072x2304x768 22.9 -> 18.8 (128x128), down 3072x768x3072 35.8 -> 29.9 and
+  // O 3072x768x768 14.0 -> 11.2 (64x64)
+  if (M >= 3072 && line_ok && !paired) {
+    if (N >= 3072) return tile_dims(L128x64);
+    if (N >= 2048) return tile_dims(L128);
+    return tile_dims(L64);
+  }
   // from M = 3072 (the batch-1 ViT, 3 images) too, measured on MI355X: up
   // 3072x3072x768 + GELU 38.1 -> 35.0 us, down 3072x768x3072 42.7 -> 34.1 us,
   // QKV and O within 0.4 us
@@ -1653,6 +1905,11 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, b
   // LDS-DMA pipeline's larger grid wins
   if (tiles(128, 128) >= kNumCU) return tile_dims(T128);
   if (!pipe_ok) return tile_dims(T64);
+  // paired epilogues below one 128x128 tile per CU, measured on MI355X (the
+  // expert at batch 32, M = 1600): the 64x64 line-DMA tile -- norm + QKV +
+  // RoPE 1600x1600x720 19.3 -> 14.5 us, norm + Q + RoPE 1600x960x720 12.2 ->
+  // 11.1
+  if (paired && line_ok) return tile_dims(L64);
   // below that, measured on MI355X: when the 64x64 grid would put one or two
   // workgroups on each CU (256-512 tiles, uneven), a 128x64 / 64x128 tile
   // halves the grid to about one per CU (expert at batch 32, M = 1600: O
@@ -1827,6 +2084,14 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s, WsKind wk = WS_ALLOCA
                             (!p.res || (p.ldr % 8 == 0 && svla_aligned16(p.res)));
   const TileCfg t = pick_tile(p.M, p.N, p.K, epi, plain, wide_rows_ok, AMODE == A_DENSE);
   if (p.norm_w && p.K > 2048) return SVLA_EINVAL;  // row statistics keep <= 2048 per row
+  // a pipelined kernel needs one full K stage, the wide one whole 4-step
+  // rounds of at least 8 steps (a strictly forced tile may violate either:
+  // refused here, before any launch)
+  const bool pipe = t.id == P128 || t.id == P64 || t.id == P128x64 || t.id == P64x128;
+  const bool line = t.id == L128 || t.id == L64 || t.id == L128x64 || t.id == L64x128;
+  if ((pipe && p.K < PBK) || (line && p.K < LBK)) return SVLA_EINVAL;
+  if (t.id == W256 && !(plain && p.K % (4 * WBK) == 0 && p.K >= 8 * WBK && wide_rows_ok))
+    return SVLA_EINVAL;
   const int gm = (p.M + t.bm - 1) / t.bm, gn = (p.N + t.bn - 1) / t.bn;
   dim3 grid(gn, gm, 1);
   if (t.id == W256) {  // persistent: one workgroup per CU walks the tiles
