@@ -24,12 +24,21 @@
  *    stream (NULL = default stream) and may be captured in a HIP graph (no
  *    memset / allocation inside).
  *  - Concurrency: calls on one stream, and replays of graphs captured from one
- *    stream, are ordered and bit-reproducible.  Running this library's kernels
- *    on two or more streams of one device at the same time is NOT supported:
- *    an experiment that ran the action expert on a second stream beside the
- *    vision encoder and prefix (with one workspace per stream, and also with
- *    the split turned off) produced wrong prefix rows in some runs, and the
- *    cause was not found.  This covers concurrent engines on one device too.
+ *    stream, are ordered and bit-reproducible.  Kernels on different streams
+ *    of one device may run at the same time (two engines' chunks replayed
+ *    concurrently on two streams equal their serial runs bit for bit), except
+ *    where a device-wide resource is shared:
+ *      * the split-K workspace of the skinny GEMMs (svla_linear_bf16) and the
+ *        static scratch array (svla_linear_scratch_bf16): split calls on
+ *        different streams must not overlap in time (svla_gemm_set_split(1)
+ *        turns splitting off);
+ *      * the fused expert (svla_expert_run) keeps one workgroup on every CU
+ *        for its whole run and they wait on each other: nothing else may run
+ *        on the device meanwhile (its waits are bounded: a launch that cannot
+ *        keep every CU ends within seconds with svla_expert_status != 0).
+ *    An earlier corruption of concurrent runs came from a race in the
+ *    pipelined GEMM and attention kernels: an LDS stage could be refilled
+ *    before a wave's reads of its previous contents had completed (fixed).
  *  - Return value: 0 on success, SVLA_EINVAL for bad shapes/alignment, or a
  *    hipError_t (positive) from the launch.
  */
@@ -136,7 +145,7 @@ int svla_layernorm_blocked_bf16(const void* x, int ldx, const void* gamma, const
  * workspace (allocated by svla_init, or by the first such call that is not
  * being graph-captured; kept until exit; a split call captured before either
  * runs unsplit) and the last workgroup of each tile sums them in a fixed
- * order.  Calls on different streams must not overlap in time (see
+ * order.  Split calls on different streams must not overlap in time (see
  * Concurrency above). */
 int svla_linear_bf16(const void* a, int lda, const void* w, int ldw, const void* bias,
                      const float* bias_f32, const void* res, int ldr, void* c, int ldc, int m,
