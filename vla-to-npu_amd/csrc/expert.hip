@@ -199,8 +199,16 @@ __device__ __forceinline__ void st2f_wt(float* p, float a, float b) {
 // Wave 0 polls the 8 sub-counters of `row` (lanes 0..7) and the status word
 // (lane 8) together until the counters sum to `target`; false when the wait
 // gave up (status set).
+//
+// (Lane-derived addresses here, in dma_w and in load_x are computed from an
+// opaque copy of the lane id, so they are not hoisted out of the phase loop:
+// the kernel runs at the 256-VGPR limit, hoisted values were spilled, and a
+// spill reload is a memory load that returns in order behind the loads
+// already issued -- the first poll, for one, waited for the wave's weight
+// requests.)
 __device__ bool wait_phase(const XArgs& g, int row, unsigned target) {
-  const int lane = threadIdx.x & 63;
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));
   const unsigned* c = lane < kSub ? g.cnt + ((size_t)row * kSub + lane) * kCntStride : g.status;
   for (int n = 0;; ++n) {
     const unsigned v = lane <= kSub ? ld_agent(c) : 0u;
@@ -278,19 +286,20 @@ __device__ __forceinline__ void wave_krange(int K, int wave, int& ks0, int& kcnt
 // other weights: the activations there are zero.
 __device__ __forceinline__ void dma_w(int epi, const bf16* W, int N, int K, int ldw, int ct,
                                       bf16* sw) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));
+  const int wave = wave_id();
   int ks0, kcnt;
   wave_krange(K, wave, ks0, kcnt);
   const int base = tile_base(epi, ct);
   const int r = lane >> 2;
   const int row = paired(epi) ? base + (r & 7) + (r >> 3) * 32 : min(base + r, N - 1);
-  const int chunk = wswz(r, lane & 3);
-  const bf16* src = W + (long)row * ldw + chunk * 8;
+  const int c8 = wswz(r, lane & 3) * 8;
+  const bf16* src = W + (long)row * ldw;
 #pragma unroll
   for (int j = 0; j < XKS; ++j) {
     if (j >= kcnt) break;  // wave-uniform
-    const int ks = ks0 + j;
-    __builtin_amdgcn_global_load_lds((void*)(src + min(ks * 32, K - 8 - chunk * 8)),
+    __builtin_amdgcn_global_load_lds((void*)(src + min((ks0 + j) * 32 + c8, K - 8)),
                                      (lds_ptr_t)(sw + j * XWSTEP), 16, 0, 0);
   }
 }
@@ -310,7 +319,9 @@ __device__ __forceinline__ void dma_gain(const bf16* norm_w, int K, bf16* gain) 
 // (only those: steps past the range are never requested); k past K reads as
 // zero.
 __device__ __forceinline__ void load_x(CPhase& P, GemmRegs& r, int t0, int t1) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));
+  const int wave = wave_id();
   const int fr = lane & 15, fk = (lane >> 4) * 8;
   int ks0, kcnt;
   wave_krange(P.K, wave, ks0, kcnt);
