@@ -55,8 +55,10 @@ def test_ops_refuse_cpu_tensors():
     (241, 960, 2560, 5),     # batch-1 prefix down: 32-column tile, split 2
     (3072, 768, 3072, 16),   # batch-1 ViT down: 64x64 line-DMA pipeline
     (3072, 3072, 768, 14),   # batch-1 ViT up: 128x64 line-DMA pipeline
-    (1600, 720, 960, 10),    # batch-32 expert O: 128x64 pipeline
+    (1600, 720, 960, 9),     # batch-32 expert O: 64x64 pipeline (short K)
+    (1600, 720, 2048, 10),   # batch-32 expert down: 128x64 pipeline (long K)
     (7712, 960, 2560, 13),   # batch-32 prefix down: 128x128 line-DMA pipeline
+    (7712, 320, 320, 16),    # batch-32 cross K/V projection: 64x64 line-DMA
     (98304, 3072, 768, 8),   # batch-32 ViT up: persistent 256x256 tile
 ])
 def test_gemm_tile_choice(m, n, k, tile):

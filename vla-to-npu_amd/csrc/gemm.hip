@@ -1862,6 +1862,10 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, b
     const long t16 = tiles(64, 16);
     if (paired) {
       if (t16 <= kNumCU) return {S16, 64, 16};
+      // past one 16-column tile per CU: the 64x64 line-DMA tile, measured on
+      // MI355X (prefix norm + QKV + RoPE 241x1600x960: 11.1 us on the 64x64
+      // LDS-DMA pipeline, 10.0 on the line tile)
+      if (K >= LBK) return tile_dims(L64);
       return pipe_ok ? tile_dims(P64) : TileCfg{S64, 64, 64};
     }
     if (t16 <= kNumCU / 2 || (K < 1536 && t16 <= kNumCU)) return {S16, 64, 16};
@@ -1875,16 +1879,19 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, b
   // 752 us; K = 3072: 1603 vs 2285 us) and loses below (K = 256: 465 vs 430)
   if (wide_ok && K >= 512 && tiles(WBM, WBN) >= 2 * kNumCU) return tile_dims(W256);
   const bool line_ok = K >= LBK;
-  // dense A from M = 4096 (the batch-32 prefix, 7712 rows), measured on
-  // MI355X: the line-DMA pipeline beats the register-staged 128x128 kernel
-  // (itself ahead of the 32-wide pipeline) -- down 7712x960x2560 60.7 ->
-  // 47.9 us and O 7712x960x960 28.8 -> 25.0 on 128x128 line tiles, norm +
-  // QKV + RoPE 7712x1600x960 54.3 -> 49.4 on 64x128; norm + gate|up + SiLU
-  // 7712x5120x960 stays on the register-staged tile (121.5 vs 121.9 us); the
-  // gathers (patch embedding, connector) keep the pipeline
+  // dense A from M = 4096 (the batch-32 prefix, 7712 rows; its RMSNorm runs
+  // on its own there), measured on MI355X with graph replay: the 128x128
+  // line-DMA tile beats the register-staged 128x128 kernel and the other
+  // pipelines on every prefix GEMM -- down 7712x960x2560 47.2 us, O
+  // 7712x960x960 25.3, QKV + RoPE 7712x1600x960 43.8 (46.7 on 64x128), gate|up
+  // + SiLU 7712x5120x960 93.4 (116.4 register-staged); a grid under one
+  // 128x128 tile per CU takes the 64x64 line tile (the cross K/V projection
+  // 7712x320x320: 9.4 -> 7.6 us); the gathers (patch embedding, connector)
+  // keep the pipeline
   if (dense && M >= 4096) {
-    if (!line_ok || epi == EPI_SILU) return tile_dims(T128);
-    return tile_dims(paired ? L64x128 : L128);
+    if (!line_ok) return tile_dims(T128);
+    if (tiles(128, 128) < kNumCU) return tile_dims(L64);
+    return tile_dims(L128);
   }
   // from M = 3072 (the batch-1 ViT, 3 images), measured on MI355X, line-DMA
   // tiles: up 3072x3072x768 + GELU 38.0 -> 27.8 us (128x64), QKV
@@ -1918,8 +1925,13 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, b
   // ViT's 576), 64x64 stays ahead.  Paired epilogues need 64-wide wave tiles:
   // 64x128, or 128x128 for large paired grids (QKV + RoPE 1600 x 720:
   // 17.7 -> 15.2 us).
+  // Re-measured with the current kernels (graph replay, M = 1600): the
+  // 128x64 tile still wins for long K (down, K = 2048: 17.8 vs 19.9 us) but
+  // not for short K (time MLP 1600x720x720: 10.3 vs 9.4 us on 64x64; O,
+  // K = 960: 11.0 vs 10.6).
   const long t64 = tiles(64, 64);
-  if (t64 >= kNumCU && t64 <= 2 * kNumCU) return tile_dims(paired ? P64x128 : P128x64);
+  if (t64 >= kNumCU && t64 <= 2 * kNumCU && (paired || K > 1024))
+    return tile_dims(paired ? P64x128 : P128x64);
   if (paired && t64 > 2 * kNumCU && tiles(128, 128) >= kNumCU / 2) return tile_dims(P128);
   return tile_dims(P64);
 }
