@@ -161,6 +161,17 @@ __device__ __forceinline__ f32x4 ldgf4(const float* p) { return *(gf4p)(p); }
 __device__ __forceinline__ uint64_t ldg64(const bf16* p) { return *(gu64cp)(p); }
 __device__ __forceinline__ uint16_t ldg16(const bf16* p) { return *(gu16cp)(p); }
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+// The thread index through an opaque copy: lane-derived values are then
+// computed where they are used instead of being hoisted out of the phase loop
+// (the kernel runs at the VGPR limit, hoisted values were spilled, and a
+// spill reload is a memory load that returns in order behind the loads
+// already issued -- the first poll of a phase, for one, waited for the wave's
+// weight requests).
+__device__ __forceinline__ int tidx() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
 
 __device__ __forceinline__ unsigned ld_agent(const unsigned* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -199,16 +210,8 @@ __device__ __forceinline__ void st2f_wt(float* p, float a, float b) {
 // Wave 0 polls the 8 sub-counters of `row` (lanes 0..7) and the status word
 // (lane 8) together until the counters sum to `target`; false when the wait
 // gave up (status set).
-//
-// (Lane-derived addresses here, in dma_w and in load_x are computed from an
-// opaque copy of the lane id, so they are not hoisted out of the phase loop:
-// the kernel runs at the 256-VGPR limit, hoisted values were spilled, and a
-// spill reload is a memory load that returns in order behind the loads
-// already issued -- the first poll, for one, waited for the wave's weight
-// requests.)
 __device__ bool wait_phase(const XArgs& g, int row, unsigned target) {
-  int lane = threadIdx.x & 63;
-  asm volatile("" : "+v"(lane));
+  const int lane = tidx() & 63;
   const unsigned* c = lane < kSub ? g.cnt + ((size_t)row * kSub + lane) * kCntStride : g.status;
   for (int n = 0;; ++n) {
     const unsigned v = lane <= kSub ? ld_agent(c) : 0u;
@@ -286,8 +289,7 @@ __device__ __forceinline__ void wave_krange(int K, int wave, int& ks0, int& kcnt
 // other weights: the activations there are zero.
 __device__ __forceinline__ void dma_w(int epi, const bf16* W, int N, int K, int ldw, int ct,
                                       bf16* sw) {
-  int lane = threadIdx.x & 63;
-  asm volatile("" : "+v"(lane));
+  const int lane = tidx() & 63;
   const int wave = wave_id();
   int ks0, kcnt;
   wave_krange(K, wave, ks0, kcnt);
@@ -307,7 +309,7 @@ __device__ __forceinline__ void dma_w(int epi, const bf16* W, int N, int K, int 
 // Norm gains of this wave's k range (at most XKS * 32 = 256 of them) into
 // the wave's gain row: one DMA instruction, issued before the phase wait.
 __device__ __forceinline__ void dma_gain(const bf16* norm_w, int K, bf16* gain) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = tidx() & 63, wave = wave_id();
   int ks0, kcnt;
   wave_krange(K, wave, ks0, kcnt);
   if (kcnt == 0) return;  // wave-uniform
@@ -319,8 +321,7 @@ __device__ __forceinline__ void dma_gain(const bf16* norm_w, int K, bf16* gain) 
 // (only those: steps past the range are never requested); k past K reads as
 // zero.
 __device__ __forceinline__ void load_x(CPhase& P, GemmRegs& r, int t0, int t1) {
-  int lane = threadIdx.x & 63;
-  asm volatile("" : "+v"(lane));
+  const int lane = tidx() & 63;
   const int wave = wave_id();
   const int fr = lane & 15, fk = (lane >> 4) * 8;
   int ks0, kcnt;
@@ -330,11 +331,9 @@ __device__ __forceinline__ void load_x(CPhase& P, GemmRegs& r, int t0, int t1) {
   for (int tm = 0; tm < 4; ++tm) rows[tm] = (unsigned)min(tm * 16 + fr, P.M - 1);
   if (P.a_f32) {
     // fp32 A (the Euler state into action_in, K <= 32: one k-step, wave 0),
-    // rounded to bf16 on the way in
+    // rounded to bf16 on the way in (only k-step 0 exists)
 #pragma unroll
-    for (int j = 0; j < XKS; ++j)
-#pragma unroll
-      for (int tm = 0; tm < 4; ++tm) r.fx[j][tm] = bf16x8{};
+    for (int tm = 0; tm < 4; ++tm) r.fx[0][tm] = bf16x8{};
     if (kcnt > 0) {
       const int k = ks0 * 32 + fk;
       // every load issued before any use (a use right after its load would
@@ -407,7 +406,7 @@ __device__ __forceinline__ bool vt_unit(CPhase& P, int ct) {
 }
 
 __device__ __forceinline__ EpiItem epi_item(CPhase& P, int ct, int t0, int t1) {
-  const int tid = threadIdx.x;
+  const int tid = tidx();
   EpiItem it{};
   const int base = tile_base(P.epi, ct);
   if (paired(P.epi)) {
@@ -558,7 +557,7 @@ __device__ __forceinline__ void vt_item(CPhase& P, int ct, const XShared& sh, in
 // one row tile)
 __device__ void vt_epilogue(CPhase& P, int ct, const XShared& sh, int t0, int t1) {
   const int nb = P.M / P.chunk;
-  for (int item = threadIdx.x; item < 256 * nb; item += XT) {
+  for (int item = tidx(); item < 256 * nb; item += XT) {
     const int tile = ((item >> 4) & 15) >> 2;  // row tile of key 4 kq at sample 0
     if (P.row_groups > 1 && (tile < t0 || tile >= t1)) continue;
     vt_item(P, ct, sh, item);
@@ -570,7 +569,7 @@ __device__ void vt_epilogue(CPhase& P, int ct, const XShared& sh, int t0, int t1
 // fragment is multiplied by them (rounded to bf16) before the MFMA
 __device__ __forceinline__ void gemm_mma(CPhase& P, const GemmRegs& r, const bf16* sw,
                                          const bf16* gain, f32x4 (&acc)[4], int t0, int t1) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = tidx() & 63, wave = wave_id();
   const int fr = lane & 15, G = lane >> 4;
   int ks0, kcnt;
   wave_krange(P.K, wave, ks0, kcnt);
@@ -592,7 +591,7 @@ __device__ __forceinline__ void gemm_mma(CPhase& P, const GemmRegs& r, const bf1
 
 // partial tile of this wave: element (row tm*16 + fr, columns 4*(lane/16) .. +3)
 __device__ __forceinline__ void put_partial(const f32x4 (&acc)[4], XShared& sh) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = tidx() & 63, wave = wave_id();
   const int fr = lane & 15;
 #pragma unroll
   for (int tm = 0; tm < 4; ++tm)
@@ -623,7 +622,7 @@ constexpr int kAttnVt = XMAXK * 64;  // V^T offset in the staging region (bf16)
 // the keys past Lk) of sample b, kv head g: 1 KB per DMA instruction, the
 // instructions dealt round the waves
 __device__ __forceinline__ void attn_stage_kv(CPhase& P, int b, int g, bf16* st) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = tidx() & 63, wave = wave_id();
   const bf16* kb = P.k + b * P.k_bs + g * 64;
   const int nki = (P.lk + 7) >> 3;
   for (int i = wave; i < nki; i += XW) {
@@ -645,7 +644,7 @@ __device__ __forceinline__ void attn_stage_kv(CPhase& P, int b, int g, bf16* st)
 // query rows r0 .. r0 + 8 n - 1 (clamped to chunk - 1) of sample b, head h
 // into LDS rows 0 .. 8 n - 1: one instruction for each of waves 0 .. n - 1
 __device__ __forceinline__ void attn_stage_q(CPhase& P, int b, int h, int r0, int n, bf16* lq) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = tidx() & 63, wave = wave_id();
   if (wave >= n) return;  // wave-uniform
   const bf16* qb = P.q + b * P.q_bs + h * 64;
   const int row = wave * 8 + (lane >> 3);
@@ -752,10 +751,7 @@ __device__ __forceinline__ void attn_solo(CPhase& P, int b, int h, int qt, int l
 
 // kv_staged: this unit's K and V^T DMA was issued already
 __device__ void attn_unit(CPhase& P, int unit, XShared& sh, bf16* st, bool kv_staged) {
-  int lane = threadIdx.x & 63;
-  // opaque: lane-derived constants are recomputed here, not hoisted out of
-  // the phase loop (where they would only be spilled)
-  asm volatile("" : "+v"(lane));
+  const int lane = tidx() & 63;
   const int wave = wave_id();
   int b, h, qt;
   attn_decode(P, unit, b, h, qt);
@@ -883,7 +879,7 @@ __device__ void attn_unit(CPhase& P, int unit, XShared& sh, bf16* st, bool kv_st
 // V^T of the cross layers' projected prefix V: unit (layer, sample, block of
 // 64 columns); thread (column d, key quad) for 4 rounds of 64 keys.
 __device__ void vt_unit_transpose(CPhase& P, int unit) {
-  const int tid = threadIdx.x;
+  const int tid = tidx();
   const int per_layer = P.vt_blocks * (P.M / P.chunk);
   const int li = unit / per_layer, rem = unit - li * per_layer;
   const int b = rem / P.vt_blocks, blk = rem - b * P.vt_blocks;
@@ -977,6 +973,7 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
   for (int p = 0; p < g.n_ph; ++p) {
     CPhase& P = g.ph[p];
     if (rank >= P.units) continue;
+    const int tid = tidx(), lane = tid & 63;  // (not hoisted: see tidx)
     const int mine = (P.units - rank + team - 1) / team;
     GemmRegs r;
     bf16* sw = s_w[wave];
