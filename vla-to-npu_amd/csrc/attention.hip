@@ -20,8 +20,11 @@ namespace {
 
 constexpr int D = 64;
 constexpr int BKEY = 64;   // keys per LDS stage
-constexpr int QW = 32;     // query rows per wave (two 16-column MFMA tiles)
-constexpr int BQ = 4 * QW; // query rows per workgroup
+// Query rows per wave: QT 16-column MFMA tiles (QT = 2: 32 rows, 128 per
+// workgroup; QT = 1 for short query ranges and small grids, see the launcher)
+template <int QT> constexpr int QW = 16 * QT;
+template <int QT> constexpr int BQ = 4 * QW<QT>;
+constexpr int kAttnCUs = 256;  // MI355X compute units
 
 struct AttnArgs {
   const bf16* q; long ldq, q_bs;
@@ -91,8 +94,9 @@ __device__ __forceinline__ v4i16 v_tr_read(const bf16* sv, int kbase, int dbase,
 // {4g..4g+3} u {16+4g..16+4g+3} in k-slots 8g..8g+7, g = lane / 16); the V^T
 // operand is read with the same key order.
 // FULL: no mask and sk % 64 == 0, so no per-score checks at all.
-template <bool FULL>
+template <bool FULL, int QT>
 __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
+  constexpr int QW = ::QW<QT>, BQ = ::BQ<QT>;
   __shared__ __attribute__((aligned(1024))) bf16 sK0[BKEY * D], sK1[BKEY * D], sK2[BKEY * D];
   __shared__ __attribute__((aligned(1024))) bf16 sV0[BKEY * D], sV1[BKEY * D], sV2[BKEY * D];
 
@@ -156,9 +160,9 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
   // Q fragments (B operand of S^T): rows qw + 16 qt + col, d = 32 ks + 8 grp.
   // Rows past sq are clamped (their outputs are never stored); loading
   // without a branch keeps the loads in flight across the DMA prologue.
-  bf16x8 qf[2][2];
+  bf16x8 qf[QT][2];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     const int qi = min(qw + qt * 16 + col, p.sq - 1);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) qf[qt][ks] = ld8(qb + (long)qi * p.ldq + ks * 32 + grp * 8);
@@ -168,25 +172,27 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
   // softmax denominator, accumulated by the MFMA with an all-ones V^T operand
   // (every row of that tile holds sum_k bf16(p[q, k]) for the lane's query q),
   // so it is rescaled with the outputs and needs no VALU sums or shuffles
-  f32x4 o[2][5];
+  f32x4 o[QT][5];
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt)
+  for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
     for (int t = 0; t < 5; ++t) o[qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
   bf16x8 ones;
 #pragma unroll
   for (int j = 0; j < 8; ++j) ones[j] = f2bf(1.0f);
-  int klim[2];  // per query tile: this lane's query sees keys < klim
-  int kmin[2];  // ... and the smallest limit over the wave (wave-uniform)
+  int klim[QT];  // per query tile: this lane's query sees keys < klim
+  int kmin[QT];  // ... and the smallest limit over the wave (wave-uniform)
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     klim[qt] = key_limit(p.mask_kind, qw + qt * 16 + col, p.sk, p.prefix_len);
     int t = klim[qt];
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) t = min(t, __shfl_xor(t, o, 64));
     kmin[qt] = __builtin_amdgcn_readfirstlane(t);
   }
-  float m_run[2] = {-INFINITY, -INFINITY};
+  float m_run[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) m_run[qt] = -INFINITY;
   const float c = p.scale_log2;
 
   auto compute = [&](auto SI, int blk) {
@@ -195,7 +201,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
     const bf16* sv = S == 0 ? sV0 : S == 1 ? sV1 : sV2;
     const int k0 = blk * BKEY;
     // S^T: 4 key subtiles x 2 query tiles, K fragments shared by both
-    f32x4 sacc[4][2];
+    f32x4 sacc[4][QT];
 #pragma unroll
     for (int ts = 0; ts < 4; ++ts) {
       bf16x8 kf[2];
@@ -203,7 +209,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
       for (int ks = 0; ks < 2; ++ks)
         kf[ks] = *reinterpret_cast<const bf16x8*>(&sk[kv_off(ts * 16 + col, ks * 32 + grp * 8)]);
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt) {
+      for (int qt = 0; qt < QT; ++qt) {
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
@@ -212,9 +218,9 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
       }
     }
     // online softmax per query tile (lane-local statistics)
-    bf16x8 pf[2][2];
+    bf16x8 pf[QT][2];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
       // only a block reaching past some query's limit needs the mask
       if (!FULL && k0 + BKEY > kmin[qt]) {
 #pragma unroll
@@ -262,11 +268,11 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
         const v4i16 w8[2] = {lo, hi};
         bf16x8 vf = *reinterpret_cast<const bf16x8*>(w8);
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
+        for (int qt = 0; qt < QT; ++qt)
           o[qt][td] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qt][kk], o[qt][td], 0, 0, 0);
       }
 #pragma unroll
-      for (int qt = 0; qt < 2; ++qt)
+      for (int qt = 0; qt < QT; ++qt)
         o[qt][4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[qt][kk], o[qt][4], 0, 0, 0);
     }
   };
@@ -314,7 +320,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
   __builtin_amdgcn_s_waitcnt(0);
 
 #pragma unroll
-  for (int qt = 0; qt < 2; ++qt) {
+  for (int qt = 0; qt < QT; ++qt) {
     const int qi = qw + qt * 16 + col;
     if (qi >= p.sq) continue;
     const float l = o[qt][4][0];
@@ -355,11 +361,22 @@ extern "C" int svla_attention_bf16(const void* q, int ldq, long q_bs, const void
   p.scale_log2 = scale * 1.4426950408889634f;
   p.mask_kind = mask_kind;
   p.prefix_len = prefix_len;
-  dim3 grid((sq + BQ - 1) / BQ, hq, batch);
-  if (mask_kind == SVLA_MASK_NONE && sk % BKEY == 0)
-    hipLaunchKernelGGL(attention_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, p);
-  else
-    hipLaunchKernelGGL(attention_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, p);
+  // 16 query rows per wave (64 per workgroup) for short query ranges and for
+  // grids that would leave the CUs with about one 128-row workgroup each;
+  // 32 rows per wave (K / V LDS reads shared by two query tiles) otherwise
+  const long g2 = (long)((sq + BQ<2> - 1) / BQ<2>) * hq * batch;
+  const bool qt1 = sq <= BQ<1> || g2 < 2 * kAttnCUs;
+  const bool full = mask_kind == SVLA_MASK_NONE && sk % BKEY == 0;
+  hipStream_t s = (hipStream_t)stream;
+  if (qt1) {
+    dim3 grid((sq + BQ<1> - 1) / BQ<1>, hq, batch);
+    if (full) hipLaunchKernelGGL((attention_kernel<true, 1>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((attention_kernel<false, 1>), grid, dim3(256), 0, s, p);
+  } else {
+    dim3 grid((sq + BQ<2> - 1) / BQ<2>, hq, batch);
+    if (full) hipLaunchKernelGGL((attention_kernel<true, 2>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((attention_kernel<false, 2>), grid, dim3(256), 0, s, p);
+  }
   SVLA_CHECK_LAUNCH();
   return SVLA_OK;
 }
