@@ -87,8 +87,10 @@ struct GemmArgs {
   // and one arrival counter per output tile (zero between calls)
   float* ws;
   unsigned* ws_cnt;
-  // persistent wide kernel: the tile grid (its launch grid is one workgroup per CU)
-  int tiles_m, tiles_n;
+  // persistent wide kernel: the tile grid (its launch grid is one workgroup per
+  // CU); w_cn > 0: each XCD keeps w_cn column blocks (see xcd_tile), else the
+  // grouped order of tile_coords
+  int tiles_m, tiles_n, w_cn;
   // slab-blocked operands / output of the wide kernel: element (row, k) of a
   // blocked [rows, K] matrix sits at (k / 32) * rows * 32 + row * 32 + k % 32,
   // so the 16 rows x 32 columns an LDS-DMA instruction fetches are one
@@ -310,6 +312,28 @@ __device__ __forceinline__ void tile_coords(int t, int gm, int gn, int& tm, int&
   const int r = t - group * per_group;
   tm = first + r % rows;
   tn = r / rows;
+}
+
+// Persistent wide kernel, column-resident order (w_cn > 0): the XCDs form
+// tiles_n / w_cn column groups, and XCD x keeps the w_cn column blocks of its
+// group (their weight panels stay in its L2 for the whole launch) and walks
+// its own contiguous range of row blocks, i-th tile of the XCD = row block
+// i / w_cn of the range, column i % w_cn of the group.  The 32 workgroups an
+// XCD runs at once then read ~32 / w_cn fresh A slices per K step and weight
+// slices that hit; the grouped order fetches both panels of a new patch at
+// every round.
+__device__ __forceinline__ int xcd_rows(const GemmArgs& p, int x, int& first) {
+  const int xg = kNumXCD * p.w_cn / p.tiles_n;  // XCDs per column group
+  const int rows = (p.tiles_m + xg - 1) / xg;
+  first = (x % xg) * rows;
+  return max(0, min(rows, p.tiles_m - first));
+}
+__device__ __forceinline__ void xcd_tile(const GemmArgs& p, int x, int i, int& tm, int& tn) {
+  const int xg = kNumXCD * p.w_cn / p.tiles_n;
+  int first;
+  xcd_rows(p, x, first);
+  tm = first + i / p.w_cn;
+  tn = (x / xg) * p.w_cn + i % p.w_cn;
 }
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int MF, int AMODE, bool NORM, int EPI,
@@ -1221,10 +1245,25 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
   // the workgroups of one XCD consecutive logical tiles, and tile_coords turns
   // those into a compact patch of row and column blocks (shared panels in
   // that XCD's L2)
-  int L = xcd_remap(blockIdx.x, G);
+  // (column-resident order: workgroup b is member b / 8 of XCD b % 8, which
+  // is where the dispatcher places it, and takes the XCD's tiles b / 8,
+  // b / 8 + G / 8, ...; the host checks that every member has one)
+  const int xcd = blockIdx.x % kNumXCD;
+  int L, Lstep, Lend;
+  if (p.w_cn > 0) {
+    int first;
+    L = blockIdx.x / kNumXCD;
+    Lstep = G / kNumXCD;
+    Lend = xcd_rows(p, xcd, first) * p.w_cn;
+  } else {
+    L = xcd_remap(blockIdx.x, G);
+    Lstep = G;
+    Lend = T;
+  }
   auto origin = [&](int l, int& m0_, int& n0_) __attribute__((always_inline)) {
     int tm_idx, tn_idx;
-    tile_coords(l, p.tiles_m, p.tiles_n, tm_idx, tn_idx);
+    if (p.w_cn > 0) xcd_tile(p, xcd, l, tm_idx, tn_idx);
+    else tile_coords(l, p.tiles_m, p.tiles_n, tm_idx, tn_idx);
     m0_ = tm_idx * WBM;
     n0_ = tn_idx * WBN;
   };
@@ -1374,8 +1413,8 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
     // the last 6 steps: the first refills this tile's K tile nk - 1, the next
     // four the next tile's K tiles 0 .. 3 (or, after the last tile, reload
     // this tile's last K tile, never read); the last refills nothing
-    const int L_next = L + G;
-    const bool has_next = L_next < T;
+    const int L_next = L + Lstep;
+    const bool has_next = L_next < Lend;
     step(I0{}, s, nk - 1, Y{}, Y{}, N{}, 0, 0);
     s = nxt(s);
     int mn0 = m0, nn0 = n0;
@@ -1789,6 +1828,28 @@ int launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
 }
 
 constexpr int kNumCU = 256;
+
+// Column blocks per XCD of the wide kernel's column-resident order (xcd_tile),
+// or 0 for the grouped order: the fewest column groups whose weight panels
+// (w_cn x 256 rows x K) fit kXcdWeightBytes of an XCD's 4 MB L2, with a tile
+// for every workgroup of every XCD.  (ViT up-projection 98304x3072x768: 6
+// column blocks, 2.4 MB, per XCD; O 98304x768x768: all 3; the QKV and down
+// projections' panels do not fit.)
+constexpr long kXcdWeightBytes = 2560L * 1024;
+int wide_cols_per_xcd(int tiles_m, int tiles_n, int K, int grid) {
+  if (grid % kNumXCD) return 0;
+  const int members = grid / kNumXCD;
+  for (int groups = 1; groups <= kNumXCD; groups *= 2) {
+    if (tiles_n % groups) continue;
+    const int cn = tiles_n / groups;
+    if ((long)cn * WBN * K * 2 > kXcdWeightBytes) continue;
+    const int xg = kNumXCD / groups;
+    const int rows = (tiles_m + xg - 1) / xg;
+    if ((tiles_m - (xg - 1) * rows) * cn < members) continue;  // the last XCD of a group
+    return cn;
+  }
+  return 0;
+}
 constexpr int kSkinnyMaxM = 256;
 
 struct TileCfg {
@@ -2110,6 +2171,7 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s, WsKind wk = WS_ALLOCA
     p.tiles_m = gm;
     p.tiles_n = gn;
     grid = dim3(min(gm * gn, kNumCU), 1, 1);
+    p.w_cn = wide_cols_per_xcd(gm, gn, p.K, (int)grid.x);
   }
   if (t.id == S32 || t.id == S64 || t.id == S16) {
     const int S = pick_split(gm * gn, p.K, t.bm, t.bn);
@@ -2250,6 +2312,7 @@ int svla_linear_wide_bf16(const void* a, int lda, const void* w, int ldw, const 
   p.tiles_m = m / WBM;
   p.tiles_n = n / WBN;
   const dim3 grid(min(p.tiles_m * p.tiles_n, kNumCU), 1, 1);
+  p.w_cn = wide_cols_per_xcd(p.tiles_m, p.tiles_n, k, (int)grid.x);
   return dispatch<A_DENSE, false>(p, EPI_STORE, act, W256, grid, (hipStream_t)stream);
 }
 
