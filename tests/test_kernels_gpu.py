@@ -188,6 +188,26 @@ def test_wide_tile_several_tiles_per_workgroup(ops, force_tile, K):
     assert_close_bf16(got_res, ops.linear(a, wp, bias=b, res=res))
 
 
+@pytest.mark.parametrize("M,N", [(24800, 3072), (30700, 768)])
+def test_wide_tile_column_resident_order(ops, force_tile, M, N):
+    """Grids where each XCD keeps a fixed set of column blocks (their weight
+    panels fit its L2) and walks its own row blocks: 97 x 12 tiles, 6 column
+    blocks per XCD and a short last row range per column group; 120 x 3
+    tiles, all 3 column blocks on every XCD; ragged last row blocks.  Checked
+    against the 128x128 pipeline kernel, bias + GELU and bias + residual."""
+    g = gen(M + N)
+    K = 768
+    a, b = randn(g, M, K).cuda(), randn(g, N, std=0.05).cuda()
+    wp = ops.pack_weight(randn(g, K, N, std=0.05).cuda())
+    res = randn(g, M, N).cuda()
+    force_tile(8)
+    got = ops.linear(a, wp, bias=b, act="gelu_tanh")
+    got_res = ops.linear(a, wp, bias=b, res=res)
+    force_tile(7)
+    assert_close_bf16(got, ops.linear(a, wp, bias=b, act="gelu_tanh"))
+    assert_close_bf16(got_res, ops.linear(a, wp, bias=b, res=res))
+
+
 def test_slab_block_roundtrip(ops):
     g = gen(40)
     x = randn(g, 300, 96).cuda()
