@@ -49,10 +49,12 @@ def test_ops_refuse_cpu_tensors():
 
 
 @pytest.mark.parametrize("m,n,k,tile", [
-    (50, 720, 960, 12),      # batch-1 expert O: 16-column skinny tile
-    (50, 720, 2048, 12),     # batch-1 expert down (split over workgroups)
-    (241, 960, 960, 12),     # batch-1 prefix O
-    (241, 960, 2560, 5),     # batch-1 prefix down: 32-column tile, split 2
+    (50, 720, 960, 17),      # layered batch-1 expert O: 32x32 small tile
+    (50, 720, 2048, 17),     # layered batch-1 expert down (no K split)
+    (241, 960, 960, 17),     # batch-1 prefix O
+    (241, 960, 2560, 17),    # batch-1 prefix down
+    (241, 320, 320, 17),     # batch-1 cross K/V projection
+    (256, 4096, 720, 4),     # past 512 small tiles: 64-column skinny tile
     (3072, 768, 3072, 16),   # batch-1 ViT down: 64x64 line-DMA pipeline
     (3072, 3072, 768, 14),   # batch-1 ViT up: 128x64 line-DMA pipeline
     (1600, 720, 960, 9),     # batch-32 expert O: 64x64 pipeline (short K)
@@ -73,6 +75,7 @@ def test_gemm_tile_choice(m, n, k, tile):
     (8, True, False),    # 256x256 pipeline: no fused-norm kernel
     (10, False, True),   # 128x64 pipeline: no paired RoPE epilogue
     (5, False, True),    # 32-column skinny tile: no paired RoPE epilogue
+    (17, False, True),   # 32x32 small tile: no paired RoPE epilogue
 ])
 def test_strict_forced_tile_without_kernel_is_einval(tile, norm, rope):
     """A strictly forced tile / epilogue pair that has no kernel returns
@@ -94,4 +97,4 @@ def test_strict_forced_tile_without_kernel_is_einval(tile, norm, rope):
     finally:
         lib.svla_gemm_set_tile(-1)
     assert rc == -22
-    assert lib.svla_gemm_set_tile(17 | 0x100) == -22
+    assert lib.svla_gemm_set_tile(19 | 0x100) == -22

@@ -308,7 +308,7 @@ def test_fused_rmsnorm_prologue(ops, M, K):
 TILES = {0: "256x256/32", 1: "128x128/32", 2: "64x128/16", 3: "64x64/16", 4: "skinny64",
          5: "skinny32", 6: "128x128/16", 7: "pipe128", 8: "wide256", 9: "pipe64",
          10: "pipe128x64", 11: "pipe64x128", 12: "skinny16", 13: "line128", 14: "line128x64",
-         15: "line64x128", 16: "line64"}
+         15: "line64x128", 16: "line64", 17: "small32", 18: "small32x64"}
 
 
 @pytest.fixture
@@ -345,11 +345,14 @@ def test_skinny_split_k_every_epilogue(ops, force_tile, force_split, tile, split
     _every_epilogue(ops, gen(200 + 10 * tile + splits), tile)
 
 
-def test_skinny_split_k_graph_replays(ops, force_split):
+def test_skinny_split_k_graph_replays(ops, force_tile, force_split):
     """Split-K calls captured in a graph: several replays with eager work in
     between, every replay equal to the eager result (the arrival counters are
-    reset by each call), then a smaller problem on the same workspace."""
+    reset by each call), then a smaller problem on the same workspace.  (The
+    32-column skinny tile is forced: the automatic choice of these shapes is
+    the unsplit 32x32 small tile.)"""
     g = gen(31)
+    force_tile(5)
     force_split(4)
     a, w = randn(g, 50, 2048), randn(g, 2048, 720, std=0.02)
     res = randn(g, 50, 720)

@@ -3,7 +3,11 @@ partials in a static device array) against ``svla_linear_bf16`` (allocated
 workspace), called through the C-ABI: bit-identical outputs on two calls in a
 row, the second with a smaller problem (whatever the first left in the
 scratch must not matter), a problem that does not split, and a split that
-needs more scratch than the array holds (SVLA_ENOSPC, nothing launched)."""
+needs more scratch than the array holds (SVLA_ENOSPC, nothing launched).
+
+The automatic tile choice no longer splits K for dense problems (their
+32-row tiles fill the chip without it), so the split cases force the skinny
+tiles that do (svla_gemm_set_tile, both entry points alike)."""
 
 import ctypes
 
@@ -39,6 +43,19 @@ def _case(M, N, K, seed, with_res=True, with_norm=True):
     return a, w, res, norm
 
 
+class _forced_tile:
+    """svla_gemm_set_tile(tile) for the duration of a with-block."""
+
+    def __init__(self, tile):
+        self.tile = tile
+
+    def __enter__(self):
+        assert _lib.load().svla_gemm_set_tile(self.tile) == 0
+
+    def __exit__(self, *exc):
+        _lib.load().svla_gemm_set_tile(-1)
+
+
 def _both(M, N, K, seed, **kw):
     a, w, res, norm = _case(M, N, K, seed, **kw)
     out_ref = torch.full((M, N), float("nan"), device="cuda", dtype=BF16)
@@ -51,9 +68,11 @@ def _both(M, N, K, seed, **kw):
 
 
 def test_scratch_entry_point_matches_linear_twice_then_smaller():
-    # 50x720x2048 splits K over 4 workgroups per tile, 20x320x1536 over 3
+    # on the 32-column skinny tile 50x720x2048 splits K over 4 workgroups per
+    # tile, 20x320x1536 over 3
     for (M, N, K), seed in (((50, 720, 2048), 1), ((20, 320, 1536), 2)):
-        ref, got = _both(M, N, K, seed)
+        with _forced_tile(5):
+            ref, got = _both(M, N, K, seed)
         assert torch.isfinite(ref).all()
         assert torch.equal(got, ref), (M, N, K)
 
@@ -65,11 +84,13 @@ def test_scratch_entry_point_unsplit_and_plain():
 
 
 def test_scratch_too_small_is_enospc():
-    # 256x2048x2048: 128 tiles of 64x64 split twice need 1.06M partial floats
+    # 256x2048x2048 on the 64-column skinny tile: 128 tiles of 64x64 split
+    # twice need 1.06M partial floats
     a, w, res, norm = _case(256, 2048, 2048, 5, with_res=False, with_norm=False)
     out = torch.zeros(256, 2048, device="cuda", dtype=BF16)
-    assert _gemm("svla_linear_scratch_bf16", a, w, out) == -28
-    torch.cuda.synchronize()
-    assert (out == 0).all()                   # nothing was launched
-    ref = torch.zeros_like(out)
-    assert _gemm("svla_linear_bf16", a, w, ref) == 0   # the allocated workspace holds it
+    with _forced_tile(4):
+        assert _gemm("svla_linear_scratch_bf16", a, w, out) == -28
+        torch.cuda.synchronize()
+        assert (out == 0).all()                   # nothing was launched
+        ref = torch.zeros_like(out)
+        assert _gemm("svla_linear_bf16", a, w, ref) == 0   # the allocated workspace holds it
