@@ -195,8 +195,8 @@ int svla_slab_block_bf16(const void* x, int ldx, void* out, int rows, int k, svl
  * pipeline, 8: 256x256 5-stage LDS-DMA pipeline with 128x128 wave tiles, 9: 64x64
  * 4-stage LDS-DMA pipeline, 10: 128x64 and 11: 64x128 4-stage LDS-DMA pipelines, 12: skinny
  * 64x16, 13: 128x128, 14: 128x64, 15: 64x128 and 16: 64x64 2-stage line-DMA pipelines
- * (64-wide K stages fetched as whole cache lines), 17: 32x32 and 18: 32x64 4-stage
- * line-DMA pipelines with K split over the waves), or -1 for the automatic
+ * (64-wide K stages fetched as whole cache lines), 17: 32x32, 18: 32x64 and 19: 96x96
+ * 4-stage line-DMA pipelines with K split over the waves), or -1 for the automatic
  * shape-based choice (default).  A forced tile that cannot serve a problem (too
  * short a K for a pipelined tile, a paired RoPE / SiLU epilogue on a tile
  * without one, anything but a plain dense store on the 256x256 pipeline) is

@@ -55,7 +55,8 @@ def test_ops_refuse_cpu_tensors():
     (241, 960, 2560, 17),    # batch-1 prefix down
     (241, 320, 320, 17),     # batch-1 cross K/V projection
     (256, 4096, 720, 4),     # past 512 small tiles: 64-column skinny tile
-    (3072, 768, 3072, 16),   # batch-1 ViT down: 64x64 line-DMA pipeline
+    (3072, 768, 3072, 19),   # batch-1 ViT down: 96x96 small tile (256 tiles)
+    (3072, 768, 768, 16),    # batch-1 ViT O: 64x64 line-DMA pipeline
     (3072, 3072, 768, 14),   # batch-1 ViT up: 128x64 line-DMA pipeline
     (1600, 720, 960, 9),     # batch-32 expert O: 64x64 pipeline (short K)
     (1600, 720, 2048, 10),   # batch-32 expert down: 128x64 pipeline (long K)
@@ -97,4 +98,4 @@ def test_strict_forced_tile_without_kernel_is_einval(tile, norm, rope):
     finally:
         lib.svla_gemm_set_tile(-1)
     assert rc == -22
-    assert lib.svla_gemm_set_tile(19 | 0x100) == -22
+    assert lib.svla_gemm_set_tile(20 | 0x100) == -22

@@ -308,7 +308,8 @@ def test_fused_rmsnorm_prologue(ops, M, K):
 TILES = {0: "256x256/32", 1: "128x128/32", 2: "64x128/16", 3: "64x64/16", 4: "skinny64",
          5: "skinny32", 6: "128x128/16", 7: "pipe128", 8: "wide256", 9: "pipe64",
          10: "pipe128x64", 11: "pipe64x128", 12: "skinny16", 13: "line128", 14: "line128x64",
-         15: "line64x128", 16: "line64", 17: "small32", 18: "small32x64"}
+         15: "line64x128", 16: "line64", 17: "small32", 18: "small32x64",
+         19: "small96"}
 
 
 @pytest.fixture

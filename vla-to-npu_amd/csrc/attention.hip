@@ -55,17 +55,24 @@ __device__ __forceinline__ int kv_off(int key, int d) {  // element offset, d % 
 typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x2_t __attribute__((ext_vector_type(2)));
 
+// Maximum of two scores as IEEE 754-2019 maximum (v_maximum3_f32 on gfx950):
+// unlike fmaxf (maxNum), which the compiler must precede with a
+// canonicalising v_max of each input, it propagates NaN and needs no quieting,
+// so a 16-score row maximum is 8 instructions and a shuffle step 1, not 10
+// and 3.  For the non-NaN scores here the two agree (masked scores are -inf).
+__device__ __forceinline__ float smax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Reductions over lanes l ^ 16 and l ^ 32 with the gfx950 row-swap VALU ops
 // (v_permlane16_swap / v_permlane32_swap): called with both operands = x,
 // every lane ends up holding {x[l], x[l ^ 16]} (resp. l ^ 32) in some order.
 // No LDS round trip, unlike a ds_bpermute shuffle.
 __device__ __forceinline__ float max_xor16(float x) {
   const u32x2_t r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return smax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float max_xor32(float x) {
   const u32x2_t r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return smax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 typedef __attribute__((address_space(3))) v4i16* lds_v4i16_ptr;
 
@@ -235,7 +242,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
 #pragma unroll
       for (int ts = 0; ts < 4; ++ts)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sacc[ts][qt][i]);
+        for (int i = 0; i < 4; ++i) mx = smax(mx, sacc[ts][qt][i]);
       mx = max_xor32(max_xor16(mx));
       // Lazy rescaling: the running maximum moves only when some query of
       // the wave sees a score more than 2^8 (in exp2 units) above it; until
@@ -244,7 +251,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
       // and the output / sum rescale is skipped for the whole wave.
       const bool grow = mx * c > m_run[qt] * c + 8.f;  // false while everything is masked
       if (__builtin_amdgcn_ballot_w64(grow)) {
-        const float m_new = fmaxf(m_run[qt], mx);
+        const float m_new = smax(m_run[qt], mx);
         const float alpha = m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
 #pragma unroll
         for (int t = 0; t < 5; ++t) o[qt][t] *= alpha;

@@ -1004,38 +1004,40 @@ __global__ __launch_bounds__(256, 2) void gemm_line_kernel(GemmArgs p) {
   pipe_epilogue<BM, BN, EPI, ACT, NORM>(p, acc, rs, m0, n0, wm, wn, fr, g);
 }
 
-// ---- small-tile GEMM: 32 x BN block tile, 4-stage line-DMA ring -------------
+// ---- small-tile GEMM: BM x BN block tile, 4-stage line-DMA ring -------------
 // For mid-size problems whose 64-row tiles leave most of the chip idle or need
 // a cross-workgroup K split (the batch-1 prefix, M = 241: 32 x 32 tiles give
-// 8 x 30 = 240 workgroups for N = 960).  Each workgroup streams 64-wide K
-// stages of its 32 A rows and BN weight rows as whole cache lines (the line
-// kernel's LDS layout and swizzle) through a 4-stage ring, three stages in
-// flight.  The 4 waves split the tile two ways and K two ways: wave w owns
-// rows 16 (w & 1) .. + 15 and every column of the tile, and computes the
-// 32-wide half (w >> 1) of each stage, so a wave holds BN / 16 accumulator
-// tiles and both halves of a stage are read once.  The two K halves meet in
-// LDS at the end; waves 0 and 1 run the epilogue (the same lane layout as the
-// pipelines: 4 consecutive columns of one row per lane).  The fused RMSNorm
-// works as in the line kernel (gain on the way into the MFMAs, row sums of
-// squares from the same fragments, 1 / rms in the epilogue), its two K halves
-// summed with the tiles.
-constexpr int SBM = 32;
+// 8 x 30 = 240 workgroups for N = 960), and tile shapes that put about one
+// tile on each CU (96 x 96 on the batch-1 ViT's 3072 x 768 outputs: 256
+// tiles).  Each workgroup streams 64-wide K stages of its BM A rows and BN
+// weight rows as whole cache lines (the line kernel's LDS layout and swizzle)
+// through a 4-stage ring, three stages in flight.  The 4 waves split the tile
+// two ways and K two ways: wave w owns rows (BM / 2) (w & 1) .. + BM / 2 - 1
+// and every column of the tile, and computes the 32-wide half (w >> 1) of
+// each stage, so every fragment of a stage is read from LDS once.  The two K
+// halves meet in LDS at the end; waves 0 and 1 run the epilogue (the same
+// lane layout as the pipelines: 4 consecutive columns of one row per lane).
+// The fused RMSNorm works as in the line kernel (gain on the way into the
+// MFMAs, row sums of squares from the same fragments, 1 / rms in the
+// epilogue), its two K halves summed with the tiles.
 constexpr int SNS = 4;  // ring stages
 
-template <int BN, int AMODE, bool NORM, int EPI, int ACT>
-__global__ __launch_bounds__(256, 2) void gemm_small_kernel(GemmArgs p) {
+template <int BM, int BN, int AMODE, bool NORM, int EPI, int ACT>
+__global__ __launch_bounds__(256, (BM * BN <= 2048 ? 2 : 1)) void gemm_small_kernel(GemmArgs p) {
+  constexpr int TM = BM / 32;          // 16-row MFMA tiles per wave
   constexpr int TN = BN / 16;          // 16-column MFMA tiles per wave
-  constexpr int B_DMA = BN / 32;       // 1 KB (8-row) weight DMA blocks per wave per stage
+  constexpr int A_DMA = BM / 32;       // 1 KB (8-row) DMA blocks per wave per stage
+  constexpr int B_DMA = BN / 32;
   constexpr bool PAIRED = EPI == EPI_ROPE || EPI == EPI_SILU;
-  static_assert(BN == 32 || BN == 64, "tile shape");
+  static_assert(BM % 32 == 0 && BN % 32 == 0 && BM <= 96 && BN <= 96, "tile shape");
   static_assert(!PAIRED || BN == 64, "paired epilogues need 64-column tiles");
-  __shared__ __attribute__((aligned(1024))) bf16 sA0[SBM * LBK], sA1[SBM * LBK],
-      sA2[SBM * LBK], sA3[SBM * LBK];
+  __shared__ __attribute__((aligned(1024))) bf16 sA0[BM * LBK], sA1[BM * LBK],
+      sA2[BM * LBK], sA3[BM * LBK];
   __shared__ __attribute__((aligned(1024))) bf16 sB0[BN * LBK], sB1[BN * LBK],
       sB2[BN * LBK], sB3[BN * LBK];
   __shared__ __attribute__((aligned(16))) bf16 s_gain[NORM ? 2048 : 8];  // K <= 2048
-  __shared__ __attribute__((aligned(16))) float s_red[2][TN * 4][64];    // K-half 1's tiles
-  __shared__ float s_ss[2][64];                                          // ... and row sums
+  __shared__ __attribute__((aligned(16))) float s_red[2][TM * TN * 4][64];  // K-half 1's tiles
+  __shared__ float s_ss[2][TM][64];                                         // ... and row sums
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, kg = wave >> 1;
@@ -1043,7 +1045,7 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(GemmArgs p) {
   const int tile = xcd_remap(blockIdx.y * gn + blockIdx.x, gn * gridDim.y);
   int tm_idx, tn_idx;
   tile_coords(tile, gridDim.y, gn, tm_idx, tn_idx);
-  const int m0 = tm_idx * SBM, n0 = tn_idx * BN;
+  const int m0 = tm_idx * BM, n0 = tn_idx * BN;
   const int nk = p.K / LBK;  // full 64-wide stages (>= 1, checked by the launcher)
 
   if constexpr (NORM) {
@@ -1052,11 +1054,15 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(GemmArgs p) {
     __syncthreads();
   }
 
-  // DMA rows: A block = wave (rows 8 wave .. + 7), weight blocks wave * B_DMA + j;
-  // lane -> row lane / 8, chunk lane % 8 at slot lswz(row, chunk)
-  const int ar = wave * 8 + (lane >> 3);
-  const int a_row = min(m0 + ar, p.M - 1), a_chunk = lswz(ar, lane & 7);
-  int b_row[B_DMA], b_chunk[B_DMA];
+  // DMA rows: block b covers rows 8b .. 8b + 7, wave w issues blocks
+  // w * X_DMA + j; lane -> row lane / 8, chunk lane % 8 at slot lswz(row, chunk)
+  int a_row[A_DMA], a_chunk[A_DMA], b_row[B_DMA], b_chunk[B_DMA];
+#pragma unroll
+  for (int j = 0; j < A_DMA; ++j) {
+    const int r = (wave * A_DMA + j) * 8 + (lane >> 3);
+    a_row[j] = min(m0 + r, p.M - 1);
+    a_chunk[j] = lswz(r, lane & 7);
+  }
 #pragma unroll
   for (int j = 0; j < B_DMA; ++j) {
     const int r = (wave * B_DMA + j) * 8 + (lane >> 3);
@@ -1068,8 +1074,11 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(GemmArgs p) {
     bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
     bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
     kt = min(kt, nk - 1);  // past the end: reload the last stage (never read)
-    const bf16* ga = a_ptr<AMODE>(p, a_row, kt * LBK + a_chunk * 8);
-    __builtin_amdgcn_global_load_lds((void*)ga, (lds_ptr_t)(sa + wave * 512), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < A_DMA; ++j) {
+      const bf16* ga = a_ptr<AMODE>(p, a_row[j], kt * LBK + a_chunk[j] * 8);
+      __builtin_amdgcn_global_load_lds((void*)ga, (lds_ptr_t)(sa + (wave * A_DMA + j) * 512), 16, 0, 0);
+    }
 #pragma unroll
     for (int j = 0; j < B_DMA; ++j) {
       const bf16* gb = p.b + (long)b_row[j] * p.ldb + kt * LBK + b_chunk[j] * 8;
@@ -1077,25 +1086,33 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(GemmArgs p) {
     }
   };
 
-  f32x4 acc[TN];
+  f32x4 acc[TN][TM];
 #pragma unroll
-  for (int i = 0; i < TN; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int fr = lane & 15, g = lane >> 4;
-  const int arow = wm * 16 + fr;  // the lane's A fragment row in the tile
-  float ssq = 0.f;
-  auto step = [&](const bf16x8 (&fw)[TN], bf16x8 fx, int k) __attribute__((always_inline)) {
+  const int arow0 = wm * (BM / 2) + fr;  // the lane's A fragment row in row tile 0
+  float ssq[TM];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm) ssq[tm] = 0.f;
+  auto step = [&](const bf16x8 (&fw)[TN], bf16x8 (&fx)[TM], int k) __attribute__((always_inline)) {
     if constexpr (NORM) {
       const bf16x8 gw = *reinterpret_cast<const bf16x8*>(&s_gain[k]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float xv = bf2f(fx[j]);
-        ssq = __builtin_fmaf(xv, xv, ssq);
-        fx[j] = f2bf(__fmul_rn(xv, bf2f(gw[j])));
-      }
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float xv = bf2f(fx[tm][j]);
+          ssq[tm] = __builtin_fmaf(xv, xv, ssq[tm]);
+          fx[tm][j] = f2bf(__fmul_rn(xv, bf2f(gw[j])));
+        }
     }
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
-      acc[tn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[tn], fx, acc[tn], 0, 0, 0);
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm)
+        acc[tn][tm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fw[tn], fx[tm], acc[tn][tm], 0, 0, 0);
   };
   // this wave's 32-wide half kg of a stage: chunks 4 kg + g
   auto compute = [&](auto SI, int kt) __attribute__((always_inline)) {
@@ -1103,13 +1120,17 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(GemmArgs p) {
     const bf16* sa = S == 0 ? sA0 : S == 1 ? sA1 : S == 2 ? sA2 : sA3;
     const bf16* sb = S == 0 ? sB0 : S == 1 ? sB1 : S == 2 ? sB2 : sB3;
     const int c = 4 * kg + g;
-    bf16x8 fw[TN];
+    bf16x8 fw[TN], fx[TM];
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
       const int r = tn * 16 + fr;
       fw[tn] = *reinterpret_cast<const bf16x8*>(&sb[r * LBK + lswz(r, c) * 8]);
     }
-    const bf16x8 fx = *reinterpret_cast<const bf16x8*>(&sa[arow * LBK + lswz(arow, c) * 8]);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) {
+      const int r = arow0 + tm * 16;
+      fx[tm] = *reinterpret_cast<const bf16x8*>(&sa[r * LBK + lswz(r, c) * 8]);
+    }
     step(fw, fx, kt * LBK + c * 8);
   };
 
@@ -1118,7 +1139,8 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(GemmArgs p) {
   // it may stay in flight), and this wave's LDS reads of the stage computed
   // before the barrier have completed, since the DMA issued right after the
   // barrier refills that stage.  gfx9 encoding, expcnt unconstrained.
-  constexpr int kWait = 0x070 | (2 * (1 + B_DMA));
+  constexpr int kWait = 0x070 | (2 * (A_DMA + B_DMA));
+  static_assert(2 * (A_DMA + B_DMA) < 16, "vmcnt field");
   auto sync_step = [&]() __attribute__((always_inline)) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(kWait);
@@ -1146,67 +1168,82 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(GemmArgs p) {
     issue(I2{}, kt + 6);
     if (kt + 3 < nk) compute(I3{}, kt + 3);
   }
-  // drain the trailing (never read) DMA before the LDS is reused or the
-  // workgroup exits
+  // drain the trailing (never read) DMA before the workgroup exits
   __builtin_amdgcn_s_waitcnt(0);
 
   // K tail (K % 64 = 8 .. 56): 32-wide steps from global memory, zero past K,
   // step t taken by the waves of K half t % 2
   for (int kb = nk * LBK + kg * 32; kb < p.K; kb += 64) {
     const int k = kb + g * 8;
-    bf16x8 fw[TN];
+    bf16x8 fw[TN], fx[TM];
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn) {
       const int n = n0 + tn * 16 + fr;
       fw[tn] = (k < p.K && n < p.N) ? ld8(p.b + (long)n * p.ldb + k) : bf16x8{};
     }
-    const bf16x8 fx = load_a<AMODE>(p, m0 + arow, k);
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) fx[tm] = load_a<AMODE>(p, m0 + arow0 + tm * 16, k);
     step(fw, fx, min(k, p.K - 8));  // fx is zero past K whatever the gain
   }
 
   // the two K halves meet: waves 2, 3 hand their tiles (and row sums) to 0, 1
-  if constexpr (NORM) ssq = xor32_sum(xor16_sum(ssq));
+  if constexpr (NORM) {
+#pragma unroll
+    for (int tm = 0; tm < TM; ++tm) ssq[tm] = xor32_sum(xor16_sum(ssq[tm]));
+  }
   if (kg == 1) {
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) s_red[wm][tn * 4 + i][lane] = acc[tn][i];
-    if constexpr (NORM) s_ss[wm][lane] = ssq;
+      for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s_red[wm][(tn * TM + tm) * 4 + i][lane] = acc[tn][tm][i];
+    if constexpr (NORM) {
+#pragma unroll
+      for (int tm = 0; tm < TM; ++tm) s_ss[wm][tm][lane] = ssq[tm];
+    }
   }
   __syncthreads();
   if (kg == 1) return;
 #pragma unroll
   for (int tn = 0; tn < TN; ++tn)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[tn][i] += s_red[wm][tn * 4 + i][lane];
-  float rs = 1.f;
-  if constexpr (NORM) rs = 1.0f / sqrtf((ssq + s_ss[wm][lane]) / (float)p.K + p.norm_eps);
+    for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[tn][tm][i] += s_red[wm][(tn * TM + tm) * 4 + i][lane];
+  float rs[TM];
+#pragma unroll
+  for (int tm = 0; tm < TM; ++tm)
+    rs[tm] = NORM ? 1.0f / sqrtf((ssq[tm] + s_ss[wm][tm][lane]) / (float)p.K + p.norm_eps) : 1.f;
 
-  // epilogue: lane holds columns n0 + 16 tn + 4 g .. + 3 of row m0 + arow;
-  // paired epilogues (RoPE / SiLU) combine tile tn < 2 with tile tn + 2 (32
-  // columns on), so only those groups load operands and store
+  // epilogue: lane holds columns n0 + 16 tn + 4 g .. + 3 of rows m0 + arow0 +
+  // 16 tm; paired epilogues (RoPE / SiLU) combine tile tn < 2 with tile tn + 2
+  // (32 columns on), so only those groups load operands and store
   constexpr int G = PAIRED ? TN / 2 : TN;
-  const int m = m0 + arow;
-  const float sc = NORM ? p.alpha * rs : p.alpha;
-  int gm[G], gnn[G];
-  EpiIn e[G];
 #pragma unroll
-  for (int t = 0; t < G; ++t) {
-    gm[t] = min(m, p.M - 1);
-    gnn[t] = min(n0 + t * 16 + 4 * g, p.N - 4);
-  }
-  epi_load_groups<EPI, G>(p, gm, gnn, e);
+  for (int tm = 0; tm < TM; ++tm) {
+    const int m = m0 + arow0 + tm * 16;
+    const float sc = NORM ? p.alpha * rs[tm] : p.alpha;
+    int gm[G], gnn[G];
+    EpiIn e[G];
 #pragma unroll
-  for (int t = 0; t < G; ++t) {
-    const int n = n0 + t * 16 + 4 * g;
-    if (m >= p.M || n >= p.N) continue;
-    float x1[4], x2[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      x1[i] = acc[t][i] * sc;
-      x2[i] = PAIRED ? acc[(t + G) % TN][i] * sc : 0.f;
+    for (int t = 0; t < G; ++t) {
+      gm[t] = min(m, p.M - 1);
+      gnn[t] = min(n0 + t * 16 + 4 * g, p.N - 4);
     }
-    epi_apply<EPI, ACT>(p, m, n, x1, x2, e[t]);
+    epi_load_groups<EPI, G>(p, gm, gnn, e);
+#pragma unroll
+    for (int t = 0; t < G; ++t) {
+      const int n = n0 + t * 16 + 4 * g;
+      if (m >= p.M || n >= p.N) continue;
+      float x1[4], x2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x1[i] = acc[t][tm][i] * sc;
+        x2[i] = PAIRED ? acc[(t + G) % TN][tm][i] * sc : 0.f;
+      }
+      epi_apply<EPI, ACT>(p, m, n, x1, x2, e[t]);
+    }
   }
 }
 
@@ -1951,7 +1988,8 @@ __global__ __launch_bounds__(256) void slab_block_kernel(const bf16* __restrict_
 // ---- launch ---------------------------------------------------------------
 enum TileId { T256 = 0, T128 = 1, T64x128 = 2, T64 = 3, S64 = 4, S32 = 5, T128S = 6,
               P128 = 7, W256 = 8, P64 = 9, P128x64 = 10, P64x128 = 11, S16 = 12, L128 = 13,
-              L128x64 = 14, L64x128 = 15, L64 = 16, N32 = 17, N32x64 = 18, NUM_TILES = 19 };
+              L128x64 = 14, L64x128 = 15, L64 = 16, N32 = 17, N32x64 = 18, N96 = 19,
+              NUM_TILES = 20 };
 
 // Launches tile configuration t; SVLA_EINVAL for a tile / epilogue pair that
 // has no kernel (the 128x64 pipeline, the 32-column skinny tile and the 32x32
@@ -2030,12 +2068,18 @@ int launch_tile(TileId t, dim3 grid, const GemmArgs& p, hipStream_t s) {
       break;
     case N32:
       if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
-        hipLaunchKernelGGL((gemm_small_kernel<32, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+        hipLaunchKernelGGL((gemm_small_kernel<32, 32, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
       else
         return SVLA_EINVAL;
       break;
     case N32x64:
-      hipLaunchKernelGGL((gemm_small_kernel<64, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      hipLaunchKernelGGL((gemm_small_kernel<32, 64, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      break;
+    case N96:
+      if constexpr (EPI != EPI_ROPE && EPI != EPI_SILU)
+        hipLaunchKernelGGL((gemm_small_kernel<96, 96, AMODE, NORM, EPI, ACT>), grid, dim3(256), 0, s, p);
+      else
+        return SVLA_EINVAL;
       break;
     default:
       return SVLA_EINVAL;
@@ -2099,6 +2143,7 @@ TileCfg tile_dims(TileId id) {
     case L64: return {L64, 64, 64};
     case N32: return {N32, 32, 32};
     case N32x64: return {N32x64, 32, 64};
+    case N96: return {N96, 96, 96};
     default: return {S32, 64, 32};
   }
 }
@@ -2122,8 +2167,10 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, b
     if ((g_force_tile == L128 || g_force_tile == L64x128) && !line_ok) return pipe_ok ? tile_dims(P128) : tile_dims(T128);
     if ((g_force_tile == L64 || g_force_tile == L128x64) && !line_ok) return pipe_ok ? tile_dims(P64) : tile_dims(T64);
     if (g_force_tile == L128x64 && paired) return tile_dims(L64);
-    if ((g_force_tile == N32 || g_force_tile == N32x64) && !line_ok) return pipe_ok ? tile_dims(P64) : tile_dims(T64);
+    const bool small = g_force_tile == N32 || g_force_tile == N32x64 || g_force_tile == N96;
+    if (small && !line_ok) return pipe_ok ? tile_dims(P64) : tile_dims(T64);
     if (g_force_tile == N32 && paired) return tile_dims(N32x64);
+    if (g_force_tile == N96 && paired) return tile_dims(N32x64);
     return tile_dims((TileId)g_force_tile);
   }
   // 32-row small tiles (gemm_small_kernel) for dense problems up to 512 rows
@@ -2138,9 +2185,16 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, b
   // tiles (norm + gate|up 241x5120x960: 12.0 on the 64x64 line tile, 13.2
   // here; expert O 1600x720x960: 9.9 vs 10.5), nor for the gathers (connector
   // 192x960x12288: 40.2 vs 47.7, patch embedding 18.8 vs 23.3).
+  // 96 x 96 small tiles for long-K problems of one such tile per CU, measured
+  // on MI355X with graph replay: the batch-1 ViT down projection 3072x768x3072
+  // 31.7 -> 27.4 us (256 tiles; its 64x64 line tile runs 576); short K loses
+  // (ViT O 3072x768x768: 12.1 -> 13.5, QKV 19.1 -> 32.1), and so do the
+  // paired / 64-column variants on every engine shape measured
+  if (dense && !paired && K >= 2048 && M >= 2048 && tiles(96, 96) <= kNumCU)
+    return tile_dims(N96);
   if (dense && M <= 512 && K >= LBK) {
-    if (!paired && tiles(SBM, 32) <= 2 * kNumCU) return tile_dims(N32);
-    if (paired && M > 128 && tiles(SBM, 64) <= 2 * kNumCU) return tile_dims(N32x64);
+    if (!paired && tiles(32, 32) <= 2 * kNumCU) return tile_dims(N32);
+    if (paired && M > 128 && tiles(32, 64) <= 2 * kNumCU) return tile_dims(N32x64);
   }
   if (M <= kSkinnyMaxM) {
     // measured on MI355X (batch-1 expert and prefix shapes): each workgroup
@@ -2398,7 +2452,7 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s, WsKind wk = WS_ALLOCA
   // refused here, before any launch)
   const bool pipe = t.id == P128 || t.id == P64 || t.id == P128x64 || t.id == P64x128;
   const bool line = t.id == L128 || t.id == L64 || t.id == L128x64 || t.id == L64x128 ||
-                    t.id == N32 || t.id == N32x64;
+                    t.id == N32 || t.id == N32x64 || t.id == N96;
   if ((pipe && p.K < PBK) || (line && p.K < LBK)) return SVLA_EINVAL;
   if (t.id == W256 && !(plain && p.K % (4 * WBK) == 0 && p.K >= 8 * WBK && wide_rows_ok))
     return SVLA_EINVAL;
