@@ -197,10 +197,16 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
     for (int o = 32; o > 0; o >>= 1) t = min(t, __shfl_xor(t, o, 64));
     kmin[qt] = __builtin_amdgcn_readfirstlane(t);
   }
-  float m_run[QT];
-#pragma unroll
-  for (int qt = 0; qt < QT; ++qt) m_run[qt] = -INFINITY;
   const float c = p.scale_log2;
+  // running maximum, the rescale threshold m_run * c + 8 and the exponent
+  // offset -(m_run * c) (0 while every score so far was masked)
+  float m_run[QT], m_thr[QT], m_off[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) {
+    m_run[qt] = -INFINITY;
+    m_thr[qt] = -INFINITY * c + 8.f;
+    m_off[qt] = -(0.f * c);
+  }
 
   auto compute = [&](auto SI, int blk) {
     constexpr int S = decltype(SI)::value;
@@ -249,21 +255,24 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
       // then the exponentials are taken against the stale maximum (values up
       // to 256, rounded to bf16 with the same relative error as values <= 1)
       // and the output / sum rescale is skipped for the whole wave.
-      const bool grow = mx * c > m_run[qt] * c + 8.f;  // false while everything is masked
+      // (the threshold m_run * c + 8 and the exponent offset are updated only
+      // when the maximum moves)
+      const bool grow = mx * c > m_thr[qt];  // false while everything is masked
       if (__builtin_amdgcn_ballot_w64(grow)) {
         const float m_new = smax(m_run[qt], mx);
         const float alpha = m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f((m_run[qt] - m_new) * c);
 #pragma unroll
         for (int t = 0; t < 5; ++t) o[qt][t] *= alpha;
         m_run[qt] = m_new;
+        m_thr[qt] = m_new * c + 8.f;
+        m_off[qt] = -((m_new == -INFINITY ? 0.f : m_new) * c);  // fully-masked-so-far guard
       }
-      const float mc = (m_run[qt] == -INFINITY ? 0.f : m_run[qt]) * c;  // fully-masked-so-far guard
 #pragma unroll
       for (int ts = 0; ts < 4; ++ts)
 #pragma unroll
         for (int i = 0; i < 4; ++i)
           pf[qt][ts >> 1][(ts & 1) * 4 + i] =
-              f2bf(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[ts][qt][i], c, -mc)));
+              f2bf(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[ts][qt][i], c, m_off[qt])));
     }
     // O^T[d, q] += V^T[d, keys] . P^T[keys, q]; V^T fragments shared by both query tiles
 #pragma unroll
