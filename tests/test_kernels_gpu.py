@@ -560,6 +560,7 @@ ATTN_CASES = [
     (2, 50, 256, 15, 5, "none", 0),     # short queries, full key blocks
     (1, 64, 320, 15, 5, "none", 0),     # largest 2-wave workgroup
     (1, 65, 65, 15, 5, "causal", 0),    # smallest 4-wave launch, mostly padding
+    (11, 1000, 1024, 12, 12, "none", 0),  # 64 query rows per wave (528 workgroups), ragged tail
 ]
 
 
