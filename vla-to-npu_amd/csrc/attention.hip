@@ -268,29 +268,34 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
         m_thr[qt] = m_new * c + 8.f;
         m_off[qt] = -((m_new == -INFINITY ? 0.f : m_new) * c);  // fully-masked-so-far guard
       }
-#pragma unroll
-      for (int ts = 0; ts < 4; ++ts)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          pf[qt][ts >> 1][(ts & 1) * 4 + i] =
-              f2bf(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[ts][qt][i], c, m_off[qt])));
     }
-    // O^T[d, q] += V^T[d, keys] . P^T[keys, q]; V^T fragments shared by both query tiles
+    // O^T[d, q] += V^T[d, keys] . P^T[keys, q]; V^T fragments shared by every
+    // query tile.  Each tile's probabilities for a 32-key half are computed
+    // right before its MFMAs, so the exponentials of one tile overlap the
+    // MFMAs of the one before.
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
+      bf16x8 vf[4];
 #pragma unroll
       for (int td = 0; td < 4; ++td) {
         const v4i16 lo = v_tr_read(sv, kk * 32 + 4 * grp, td * 16, col);
         const v4i16 hi = v_tr_read(sv, kk * 32 + 16 + 4 * grp, td * 16, col);
         const v4i16 w8[2] = {lo, hi};
-        bf16x8 vf = *reinterpret_cast<const bf16x8*>(w8);
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-          o[qt][td] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qt][kk], o[qt][td], 0, 0, 0);
+        vf[td] = *reinterpret_cast<const bf16x8*>(w8);
       }
 #pragma unroll
-      for (int qt = 0; qt < QT; ++qt)
+      for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            pf[qt][kk][h * 4 + i] =
+                f2bf(__builtin_amdgcn_exp2f(__builtin_fmaf(sacc[2 * kk + h][qt][i], c, m_off[qt])));
+#pragma unroll
+        for (int td = 0; td < 4; ++td)
+          o[qt][td] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[td], pf[qt][kk], o[qt][td], 0, 0, 0);
         o[qt][4] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[qt][kk], o[qt][4], 0, 0, 0);
+      }
     }
   };
 
