@@ -2237,8 +2237,13 @@ TileCfg pick_tile(int M, int N, int K, int epi, bool plain, bool wide_rows_ok, b
   // 7712x960x960 25.3, QKV + RoPE 7712x1600x960 43.8 (46.7 on 64x128), gate|up
   // + SiLU 7712x5120x960 93.4 (116.4 register-staged); a grid under one
   // 128x128 tile per CU takes the 64x64 line tile (the cross K/V projection
-  // 7712x320x320: 9.4 -> 7.6 us); the gathers (patch embedding, connector)
-  // keep the pipeline
+  // 7712x320x320: 9.4 -> 7.6 us).
+  // The gathers from M = 4096 (the batch-32 patch embedding 98304x768x768
+  // and pixel-shuffle connector 6144x960x12288), measured on MI355X with
+  // graph replay: the register-staged 128x128 kernel -- patch 311 -> 219 us,
+  // connector 310 -> 211 us against the 64x64 line tile the M >= 3072 rule
+  // below would take (the 128x128 LDS-DMA pipeline: 235 / 210 us)
+  if (!dense && M >= 4096) return tile_dims(T128);
   if (dense && M >= 4096) {
     if (!line_ok) return tile_dims(T128);
     if (tiles(128, 128) < kNumCU) return tile_dims(L64);
