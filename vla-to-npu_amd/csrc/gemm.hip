@@ -1014,8 +1014,9 @@ __global__ __launch_bounds__(256, 2) void gemm_line_kernel(GemmArgs p) {
 // through a 4-stage ring, three stages in flight.  The 4 waves split the tile
 // two ways and K two ways: wave w owns rows (BM / 2) (w & 1) .. + BM / 2 - 1
 // and every column of the tile, and computes the 32-wide half (w >> 1) of
-// each stage, so every fragment of a stage is read from LDS once.  The two K
-// halves meet in LDS at the end; waves 0 and 1 run the epilogue (the same
+// each stage, so each activation fragment of a stage is read from LDS once
+// and each weight fragment twice (once per row half).  The two K halves meet
+// in LDS at the end; waves 0 and 1 run the epilogue (the same
 // lane layout as the pipelines: 4 consecutive columns of one row per lane).
 // The fused RMSNorm works as in the line kernel (gain on the way into the
 // MFMAs, row sums of squares from the same fragments, 1 / rms in the
