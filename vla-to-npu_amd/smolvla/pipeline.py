@@ -111,8 +111,13 @@ class SmolVLAEngine:
         self.kv = [z(B * L, d.q_dim + 2 * d.kv_dim) for _ in range(cfg.prefix_layers)]
         self.pbufs = layers.Buffers(dev)
         # expert
-        self.cross = {i: (z(B * L, e.kv_dim), z(B * L, e.kv_dim))
-                      for i in range(cfg.expert_layers) if cfg.is_cross(i)}
+        # projected cross K | V of a layer side by side in one buffer (one GEMM
+        # projects both, layers.cross_kv)
+        self.cross = {}
+        for i in range(cfg.expert_layers):
+            if cfg.is_cross(i):
+                ckv = z(B * L, 2 * e.kv_dim)
+                self.cross[i] = (ckv[:, :e.kv_dim], ckv[:, e.kv_dim:])
         M = B * cfg.chunk
         self.x_t = z(M, cfg.action_dim, dt=F32)
         self.x_bf = z(M, cfg.action_dim)
