@@ -221,3 +221,27 @@ def test_vit_layer_wide_blocked(biases):
     finally:
         lib.svla_gemm_set_tile(-1)
     assert torch.equal(xr, xg)
+
+
+@pytest.mark.parametrize("rows", [241, 482])
+def test_cross_kv_block_diagonal_equals_two_projections(rows):
+    """Prefix K | V side by side (the KV cache rows) projected by one GEMM on
+    the block-diagonal weight equals the two separate projections bit for bit
+    (the zero blocks add exact zeros), and both match the oracle's cross_kv
+    products (vla/action_expert_bf16.py:757-758)."""
+    from smolvla import layers
+    from smolvla.vla.action_expert_bf16 import DEFAULT_CFG
+    p = expert_cross_layer_params(_Gen(116, norm_init="random"), DEFAULT_CFG, 320)
+    P = layers.prep_cross(p, "cuda")
+    kv = x_in(117, rows, 1600).cuda()             # [.. | K | V] as the prefix cache holds it
+    k_src, v_src = kv[:, 960:1280], kv[:, 1280:]
+    ckv = torch.zeros(rows, 640, dtype=BF16, device="cuda")
+    ck, cv = layers.cross_kv(k_src, v_src, P, out_k=ckv[:, :320], out_v=ckv[:, 320:])
+    sep_k = torch.zeros(rows, 320, dtype=BF16, device="cuda")
+    sep_v = torch.zeros(rows, 320, dtype=BF16, device="cuda")
+    layers.cross_kv(k_src, v_src, P, out_k=sep_k, out_v=sep_v)  # separate outputs: two GEMMs
+    assert torch.equal(ck, sep_k) and torch.equal(cv, sep_v)
+    want_k = ref.linear(k_src.cpu(), p["Wk_cross"])
+    want_v = ref.linear(v_src.cpu(), p["Wv_cross"])
+    check(ck, want_k)
+    check(cv, want_v)
