@@ -1266,8 +1266,9 @@ __global__ __launch_bounds__(256, (BM * BN <= 2048 ? 2 : 1)) void gemm_small_ker
 // AGPR operand: with the builtin, the register allocator shuffles AGPR-resident
 // loop accumulators with v_accvgpr_mov copies every iteration (measured: more
 // than half of the MFMA rate lost).  The asm is opaque to the hazard
-// recognizer, so the kernel inserts the wait states itself: before the first
-// MFMA reads the zeroed accumulators and before the epilogue reads results.
+// recognizer, so the kernel inserts the wait states itself, before the
+// epilogue reads results.  A tile's first K step takes srcC = 0, so the
+// accumulators are never zeroed by VALU writes.
 constexpr int WBM = 256, WBN = 256, WBK = 32;
 constexpr int W_DMA = 4;  // 1 KB DMA blocks per wave per operand per stage
 constexpr int W_STAGES = 5;                    // LDS ring depth
@@ -1292,6 +1293,11 @@ __device__ __forceinline__ void static_for(F&& f) {
 
 __device__ __forceinline__ void mfma_agpr(f32x4& acc, const bf16x8& a, const bf16x8& b) {
   asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(acc) : "v"(a), "v"(b));
+}
+// The first K step of a tile: srcC is the inline constant 0, so the
+// accumulators need no zeroing pass (256 VALU writes per wave and tile).
+__device__ __forceinline__ void mfma_agpr_first(f32x4& acc, const bf16x8& a, const bf16x8& b) {
+  asm volatile("v_mfma_f32_16x16x32_bf16 %0, %1, %2, 0" : "=a"(acc) : "v"(a), "v"(b));
 }
 
 // Redefines every accumulator (no instruction emitted): uses of acc after this
@@ -1357,6 +1363,18 @@ __device__ __forceinline__ void wide_addend(const GemmArgs& p, int wn0, int g,
 // activations: 0.45 / 0.6 GB at batch 32), where they measured 6-8% faster;
 // in-place residual updates keep ordinary stores (the residual stream is
 // re-read right away).
+// bf16 rounding of two values with one conversion (v_cvt_pk_bf16_f32, round
+// to nearest even like the compiler's own), back to fp32 by a shift and a
+// mask: rbf(a), rbf(b).  Written as asm because the compiler splits a
+// two-element conversion whose halves are used separately into two
+// single-element conversions.
+__device__ __forceinline__ void rbf_pair(float a, float b, float& ra, float& rb) {
+  unsigned u;
+  asm("v_cvt_pk_bf16_f32 %0, %1, %2" : "=v"(u) : "v"(a), "v"(b));
+  ra = __uint_as_float(u << 16);
+  rb = __uint_as_float(u & 0xffff0000u);
+}
+
 template <int ACT, bool RES>
 __device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WTN][WTM],
                                               const bf16x4 (&braw)[WTN], bf16* st, int wm0,
@@ -1395,11 +1413,19 @@ __device__ __forceinline__ void wide_epilogue(const GemmArgs& p, f32x4 (&acc)[WT
       for (int h = 0; h < 2; ++h) {
         const int tm = 2 * c + h;
         bf16x4 o;
+        float v[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = __builtin_fmaf(acc[tn][tm][i], alpha, cb[tn][i]);
-          if constexpr (ACT != SVLA_ACT_NONE) o[i] = f2bf(apply_act<ACT>(rbf(v)));
-          else o[i] = f2bf(v);
+        for (int i = 0; i < 4; ++i) v[i] = __builtin_fmaf(acc[tn][tm][i], alpha, cb[tn][i]);
+        if constexpr (ACT != SVLA_ACT_NONE) {
+          // the activation's input rounded to bf16 two at a time
+          float x[4];
+          rbf_pair(v[0], v[1], x[0], x[1]);
+          rbf_pair(v[2], v[3], x[2], x[3]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = f2bf(apply_act<ACT>(x[i]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = f2bf(v[i]);
         }
         *reinterpret_cast<bf16x4*>(st_addr(h * 16 + fr, tn * 4 + g)) = o;
       }
@@ -1546,19 +1572,9 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
                                        16, 0, 0);
   };
 
+  // accumulators: defined by each tile's first K step (srcC = 0), so they are
+  // never zeroed
   f32x4 acc[WTN][WTM];
-  auto zero_acc = [&]() __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < WTN; ++i)
-#pragma unroll
-      for (int j = 0; j < WTM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    // zeroed accumulators are written by VALU; the first MFMA reads them as
-    // srcC.  The empty asm statements redefine every accumulator, and
-    // volatile asm keeps its order, so the zeroing cannot sink below the
-    // wait states.
-    pin_accumulators(acc);
-    asm volatile("s_nop 4");
-  };
 
   // fragment f of a stage: f < WTN -> weight tile f, else activation tile f - WTN
   const int fr = lane & 15, g = lane >> 4;
@@ -1610,7 +1626,10 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
     }
 #pragma unroll
     for (int i = 0; i < WTN * WTM; ++i) {
-      mfma_agpr(acc[i / WTM][i % WTM], fw[R][i / WTM], fx[R][i % WTM]);
+      if constexpr (decltype(EXTRA)::value)  // the tile's first step
+        mfma_agpr_first(acc[i / WTM][i % WTM], fw[R][i / WTM], fx[R][i % WTM]);
+      else
+        mfma_agpr(acc[i / WTM][i % WTM], fw[R][i / WTM], fx[R][i % WTM]);
       if constexpr (decltype(REFILL)::value)
         if (i < 32 && i % 4 == 0) issue_one(s, i / 4, kt);
       if constexpr (decltype(READ)::value)
@@ -1626,7 +1645,6 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < 2 * W_DMA; ++j) issue_one(s, j, s);
   }
-  zero_acc();
   __builtin_amdgcn_s_waitcnt(kWaitPrologue);
   __builtin_amdgcn_s_barrier();
 #pragma unroll
@@ -1689,7 +1707,6 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
     n0 = nn0;
     s0 = nxt(s);   // the next tile's K tile 0
     pend_kt = 4;   // goes into stage s, after the next step's barrier
-    zero_acc();
     static_for<0, WTN + WTM>([&](auto F) { read_one(s0, I0{}, decltype(F)::value); });
   }
   // drain the trailing (never read) DMA and the stores before exit
