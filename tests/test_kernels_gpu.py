@@ -243,6 +243,31 @@ def test_linear_wide_layouts(ops, force_tile, layout):
     assert_close_bf16(want, ref.gelu(ref.linear(a.cpu(), w.cpu(), b.cpu()), "tanh"))
 
 
+@pytest.mark.parametrize("act,alpha", [("gelu_erf", 1.0), ("silu", 1.0), ("silu", 0.5),
+                                       ("gelu_tanh", 0.25), (None, 0.5)])
+def test_linear_wide_epilogues(ops, force_tile, act, alpha):
+    """Every activation of the wide kernel's epilogue, with and without a
+    scale, is bit-for-bit the (forced) 128x128 kernel's result; the wide
+    kernel rounds the scaled, biased value to bf16 two values per conversion
+    before the activation, the 128x128 kernel one at a time."""
+    g = gen(77)
+    M, N, K = 768, 512, 640
+    a, w, b = randn(g, M, K).cuda(), randn(g, K, N, std=0.05).cuda(), randn(g, N, std=0.05).cuda()
+    wp = ops.pack_weight(w)
+    force_tile(8)
+    want = ops.linear(a, wp, bias=b, act=act, alpha=alpha)
+    force_tile(-1)
+    got = ops.linear_wide(ops.slab_block(a), ops.slab_block(wp), M, N, K, bias=b, act=act,
+                          alpha=alpha, layout=ops.LAYOUT_A_BLOCKED | ops.LAYOUT_W_BLOCKED)
+    assert torch.equal(got, want)
+    # fp32 affine part rounded once to bf16, then the activation in fp32
+    lin = (ref.linear(a.cpu().float(), w.cpu().float()) * alpha + b.cpu().float()).bfloat16()
+    lin = lin.float()
+    exp = {None: lambda x: x, "silu": ref.silu, "gelu_erf": lambda x: ref.gelu(x, "none"),
+           "gelu_tanh": lambda x: ref.gelu(x, "tanh")}[act](lin)
+    assert_close_bf16(got, exp)
+
+
 def test_linear_wide_rejects_bad_shapes(ops):
     a = torch.zeros(300, 384, dtype=BF16, device="cuda")
     w = torch.zeros(768, 384, dtype=BF16, device="cuda")
