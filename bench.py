@@ -19,7 +19,13 @@ Prints ONE JSON line:
                launch time from HIP events on its stream, against the 2.5 PFLOP/s
                dense bf16 (or 8 TB/s HBM) peak
   cpu_baseline the CPU oracle (PyTorch bf16 restatement of the reference
-               modules) timed on this host's cores on a bounded sample
+               modules) timed on this host's cores on a bounded sample of
+               bs=1 chunks (the bs=32 CPU rate extrapolated as bs=1 x 32)
+  configs_bs1  BASELINE configs 0-3 at batch 1: GPU latency (HIP-graph
+               replays), roofline floor and fraction, and the CPU oracle's
+               time for the same config in the same run, with its threads
+  output_check the timed engine's actions are finite and sample 0 matches the
+               batch-1 engine (checked outside every timed region)
 """
 
 from __future__ import annotations
@@ -41,6 +47,8 @@ import torch  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+# final actions, engine vs engine or vs the oracle (the chunk tests' bound)
+OUTPUT_ATOL = 5e-2
 
 
 def log(msg):
@@ -271,9 +279,224 @@ def cpu_baseline(cfg, params, seconds):
                 break
     return {"value": round(n / el, 4), "unit": "chunks/s", "cores": torch.get_num_threads(),
             "kind": "port", "cpu_model": cpu_model(), "host_cpus": os.cpu_count(),
+            "batch": 1, "extrapolated": "bs=1 x 32: the batch-32 CPU rate is taken as the "
+                                        "measured bs=1 chunk rate (samples are independent)",
             "sample": f"{n} full bs=1 chunks (3x512^2 cameras, 241-token prefix, 10 Euler "
-                      f"steps) in {el:.1f} s, torch {torch.__version__} bf16 on CPU",
+                      f"steps) in {el:.1f} s, torch {torch.__version__} bf16 on CPU; "
+                      f"reported as the bs=32 rate by bs=1 x 32 extrapolation",
             "ms_per_chunk": round(el / n * 1e3, 1)}
+
+
+def _tree_bytes(tree):
+    """bf16 bytes of every tensor in a (nested) params tree."""
+    n, stack = 0, [tree]
+    while stack:
+        x = stack.pop()
+        if isinstance(x, dict):
+            stack.extend(x.values())
+        elif isinstance(x, (list, tuple)):
+            stack.extend(x)
+        elif torch.is_tensor(x):
+            n += 2 * x.numel()
+    return n
+
+
+def graph_ms(fn, reps=50, warm=3):
+    """(median, min) ms of ``reps`` HIP-graph replays of ``fn``'s launches."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(warm):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warm):
+        g.replay()
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        ts.append(a.elapsed_time(b))
+    del g
+    return statistics.median(ts), min(ts)
+
+
+def config_work(cfg, params):
+    """(flops, bytes) of BASELINE configs 0-3 at batch 1: FLOPs as in
+    ``chunk_flops`` (attention dense); bytes = every weight the config reads
+    once plus its inputs and outputs."""
+    from smolvla import census
+    v, d, e = cfg.vit, cfg.decoder, cfg.expert
+    T, H = v.tokens, v.hidden
+
+    def dec_flops(L, dc):
+        return (2 * L * (dc.q_dim + 2 * dc.kv_dim) * dc.hidden + 2 * L * dc.hidden * dc.q_dim
+                + 3 * 2 * L * dc.inter * dc.hidden + 4 * L * L * dc.n_q_heads * 64)
+
+    L0, Lp = 128, cfg.prefix_len
+    vit = (2 * T * (3 * H) * H + 2 * T * H * H + 2 * 2 * T * v.inter * H
+           + 4 * T * T * v.n_heads * 64)
+    patch = 2 * T * H * (v.channels * v.patch ** 2)
+    conn = cfg.n_cameras * 2 * cfg.image_tokens * d.hidden * H * cfg.pixel_shuffle ** 2
+    kv_bytes = 2 * Lp * 2 * d.kv_dim
+    n_cross = sum(cfg.is_cross(i) for i in range(cfg.expert_layers))
+    step_b = census.expert_step_weight_bytes(cfg) + n_cross * 2 * Lp * 2 * e.kv_dim
+    return {
+        "cfg0": (dec_flops(L0, d), _tree_bytes(params["prefix"][0]) + 2 * L0 * (2 * d.hidden + 2 * d.kv_dim)),
+        "cfg1": (v.layers * vit + patch, _tree_bytes([params["vit"], params["patch"]])
+                 + 2 * (v.channels * v.image ** 2 + T * H)),
+        "cfg2": (conn + cfg.prefix_layers * dec_flops(Lp, d) + 2 * d.hidden * cfg.state_dim,
+                 _tree_bytes([params["connector"], params["prefix"], params["state"]])
+                 + 2 * (cfg.n_cameras * T * H + cfg.lang_tokens * d.hidden)
+                 + cfg.prefix_layers * kv_bytes),
+        "cfg3_step": (census.expert_step_flops(cfg, 1), step_b),
+        "cfg3_loop": (cfg.num_steps * census.expert_step_flops(cfg, 1), cfg.num_steps * step_b),
+    }
+
+
+CONFIG_NAMES = {
+    "cfg0": "config 0: one SmolLM2 decoder block, 128 tokens, causal, KV out",
+    "cfg1": "config 1: SigLIP ViT per image (patch embed + 12 blocks, 1024 tokens)",
+    "cfg2": "config 2: connector x3 cameras + 241-token prefix x16 layers with KV cache",
+    "cfg3_step": "config 3: one Euler step of the 16-layer action expert (layer by layer)",
+    "cfg3_loop": "config 3: the 10-step expert loop (the fused batch-1 launch)",
+}
+
+
+def gpu_configs(cfg, params, e1):
+    """BASELINE configs 0-3 at batch 1 on the GPU, on the prepared weights of
+    the batch-1 engine ``e1``: each config's launches captured in one HIP
+    graph, median of 50 replays."""
+    from smolvla import layers, ops
+    v, d = cfg.vit, cfg.decoder
+    dev = e1.device
+    g = torch.Generator(device=dev).manual_seed(11)
+    # cfg0: the prefix's layer-0 weights at 128 tokens, causal
+    x0 = torch.randn(128, d.hidden, generator=g, device=dev).to(torch.bfloat16)
+    x = torch.empty_like(x0)
+    kv = torch.empty(128, d.q_dim + 2 * d.kv_dim, dtype=torch.bfloat16, device=dev)
+    rope128 = layers.Rope.make(128, d.head_dim, d.rope_theta, dev)
+    bufs0 = layers.Buffers(dev)
+
+    def cfg0():
+        x.copy_(x0)
+        layers.decoder_layer(x, e1.prefix[0], d, 1, 128, rope128, "causal", 0, bufs0, qkv_out=kv)
+
+    img = e1.in_images[:1]
+    vx = torch.empty(v.tokens, v.hidden, dtype=torch.bfloat16, device=dev)
+    bufs1 = layers.Buffers(dev)
+
+    def cfg1():
+        ops.patch_embed(img, e1.patch_w, e1.patch_b, e1.pos_emb, v.patch, out=vx)
+        for P in e1.vit:
+            layers.vit_layer(vx, P, v, 1, v.tokens, bufs1)
+
+    def cfg2():
+        e1.build_prefix()
+        e1.run_prefix()
+
+    dt = -1.0 / cfg.num_steps
+
+    def cfg3_step():
+        e1.expert_step(0, dt)
+
+    def cfg3_loop():
+        e1.x_t.copy_(e1.in_noise.view(-1, cfg.action_dim))
+        e1.fx.run()
+
+    out = {}
+    for name, fn in (("cfg0", cfg0), ("cfg1", cfg1), ("cfg2", cfg2), ("cfg3_step", cfg3_step),
+                     ("cfg3_loop", cfg3_loop)):
+        if name == "cfg3_loop" and e1.fx is None:
+            continue
+        med, mn = graph_ms(fn)
+        out[name] = (med, mn)
+        log(f"{name}: {med:.3f} ms (GPU, batch 1)")
+    e1.check()
+    return out
+
+
+def cpu_configs(cfg, params, seconds=3.0):
+    """The CPU oracle on BASELINE configs 0-3 at batch 1 (bf16, this host's
+    cores): median of repeats until ``seconds`` per config (at least 3)."""
+    import oracle.smolvla_ref as ref
+    from smolvla.params import smolvla_inputs
+    torch.set_num_threads(min(os.cpu_count() or 1, int(os.environ.get("OMP_NUM_THREADS", "64"))))
+    g = torch.Generator().manual_seed(11)
+    d, v = cfg.decoder, cfg.vit
+    x0 = torch.randn(1, 128, d.hidden, generator=g).to(torch.bfloat16)
+    images, ids, state, noise = smolvla_inputs(cfg, 1, seed=7)
+    vis = torch.randn(1, cfg.n_cameras, v.tokens, v.hidden, generator=g).to(torch.bfloat16)
+    with torch.inference_mode():
+        prefix = ref.build_prefix(vis, ids, state, params, cfg)
+        _, kvc = ref.prefix_forward(prefix, params, cfg)
+        ckv = ref.cross_kv(kvc, params, cfg)
+
+    def vit1():
+        y = ref.patch_embed(images[0, :1], params["patch"]["kernel"], params["patch"]["bias"],
+                            params["patch"]["pos_emb"])
+        for lp in params["vit"]:
+            y = ref.vit_block(y, lp, v)
+        return y
+
+    def pre():
+        p = ref.build_prefix(vis, ids, state, params, cfg)
+        return ref.prefix_forward(p, params, cfg)
+
+    def loop():
+        x, t = noise.clone(), 1.0
+        for _ in range(cfg.num_steps):
+            x = x + (-1.0 / cfg.num_steps) * ref.expert_velocity(x, t, ckv, params, cfg).float()
+            t -= 1.0 / cfg.num_steps
+        return x
+
+    fns = {"cfg0": lambda: ref.decoder_block(x0, params["prefix"][0], d, "causal"),
+           "cfg1": vit1, "cfg2": pre,
+           "cfg3_step": lambda: ref.expert_velocity(noise, 1.0, ckv, params, cfg),
+           "cfg3_loop": loop}
+    out = {}
+    with torch.inference_mode():
+        for name, fn in fns.items():
+            fn()                                   # warm-up
+            ts, t_end = [], time.perf_counter() + seconds
+            while len(ts) < 3 or (time.perf_counter() < t_end and len(ts) < 20):
+                t0 = time.perf_counter()
+                fn()
+                ts.append((time.perf_counter() - t0) * 1e3)
+            out[name] = (statistics.median(ts), len(ts))
+            log(f"{name}: {out[name][0]:.1f} ms (CPU oracle, {torch.get_num_threads()} threads)")
+    return out, torch.get_num_threads()
+
+
+def config_lines(cfg, params, gpu, cpu, threads):
+    work = config_work(cfg, params)
+    lines = {}
+    for name, (med, mn) in gpu.items():
+        fl, by = work[name]
+        t_mfma = fl / (PEAK_BF16_TFLOPS * 1e12) * 1e6
+        t_hbm = by / (PEAK_HBM_GBS * 1e9) * 1e6
+        floor = max(t_mfma, t_hbm)
+        row = {"what": CONFIG_NAMES[name], "batch": 1, "gpu_ms_median": round(med, 4),
+               "gpu_ms_min": round(mn, 4), "flops": fl, "bytes": by,
+               "tflops": round(fl / (med * 1e-3) / 1e12, 2),
+               "gbs": round(by / (med * 1e-3) / 1e9, 1),
+               "roofline": {"bound": "mfma" if t_mfma >= t_hbm else "hbm",
+                            "floor_us": round(floor, 2), "frac": round(floor / (med * 1e3), 4)}}
+        if cpu and name in cpu:
+            row["cpu_ms_median"] = round(cpu[name][0], 2)
+            row["cpu_reps"] = cpu[name][1]
+            row["cpu_threads"] = threads
+            row["gpu_speedup_vs_cpu"] = round(cpu[name][0] / med, 1)
+        lines[name] = row
+    return lines
 
 
 def write_kernel_table(cfg, params, batch):
@@ -317,6 +540,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-latency", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config (BASELINE configs 0-3, batch 1) lines")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only launch the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
@@ -352,7 +577,8 @@ def main():
     B = args.batch
     log(f"preparing engine at batch {B}")
     eng = SmolVLAEngine(cfg, params, batch=B)
-    eng.load_inputs(*smolvla_inputs(cfg, B, seed=1, device="cuda"))
+    inp = smolvla_inputs(cfg, B, seed=1, device="cuda")
+    eng.load_inputs(*inp)
     eng.capture()
     log(f"warmup {args.warmup}")
     for _ in range(args.warmup):
@@ -369,16 +595,30 @@ def main():
     flops = chunk_flops(cfg, B)
     log(f"batch {B}: {ms_step:.2f} ms/chunk-batch, {value:.1f} chunks/s, "
         f"{flops / (ms_step * 1e-3) / 1e12:.1f} TFLOP/s end to end")
+    # the timed replays' result (inputs unchanged since the first replay)
+    timed_out = eng.x_t.view(B, cfg.chunk, cfg.action_dim)[0].clone()
+    eng.check()
     roof, _ = dominant_roofline(eng)
     log(f"dominant kernel: {roof['kernel']}, {roof['avg_launch_us']} us/launch x "
         f"{roof['launches_per_chunk']}, {roof['achieved']} {roof['unit']}")
     del eng
     torch.cuda.empty_cache()
 
+    # output check, outside every timed region: the timed engine's actions are
+    # finite and sample 0 equals what the batch-1 engine (other kernels: the
+    # fused expert, batch-1 tiles) computes from the same inputs
+    e1 = SmolVLAEngine(cfg, params, batch=1)
+    one = e1.run(*[t[:1] for t in inp])[0]
+    check = {"finite": bool(torch.isfinite(timed_out).all().item()),
+             "sample0_max_abs_vs_bs1_engine": round((one - timed_out).abs().max().item(), 5),
+             "atol": OUTPUT_ATOL}
+    log(f"output check: {check}")
+    if not check["finite"] or check["sample0_max_abs_vs_bs1_engine"] > OUTPUT_ATOL:
+        raise SystemExit(f"bench: the timed engine's actions fail the output check {check}")
+
     lat = None
     if not args.no_latency:
         log("latency engine at batch 1")
-        e1 = SmolVLAEngine(cfg, params, batch=1)
         e1.load_inputs(*smolvla_inputs(cfg, 1, seed=2, device="cuda"))
         e1.capture()
         time_chunks(e1, 10)
@@ -392,15 +632,21 @@ def main():
                             "achieved_tflops": round(fl / (med * 1e-3) / 1e12, 1),
                             "achieved_gbs": round(by / (med * 1e-3) / 1e9, 1),
                             "flops": fl, "bytes": by, "frac": round(floor_us / (med * 1e3), 4)}}
+        e1.check()
         log(f"batch 1 latency: median {lat['ms_per_chunk_median']} ms")
-        del e1
-        torch.cuda.empty_cache()
+    gpu_cfg = None if args.no_configs else gpu_configs(cfg, params, e1)
+    del e1
+    torch.cuda.empty_cache()
 
     cpu = None
+    cpu_cfg, threads = None, None
     if not args.no_cpu:
         log(f"CPU oracle baseline (~{args.cpu_seconds:.0f} s)")
         cpu = cpu_baseline(cfg, params, args.cpu_seconds)
         log(f"CPU: {cpu['value']} chunks/s on {cpu['cores']} threads")
+        if gpu_cfg:
+            cpu_cfg, threads = cpu_configs(cfg, params)
+    configs = config_lines(cfg, params, gpu_cfg, cpu_cfg, threads) if gpu_cfg else None
 
     line = {
         "metric": "ms per 50-step action chunk @bs1; chunks/s @bs32; % MFMA/HBM roofline",
@@ -413,7 +659,9 @@ def main():
                                "48 lang tokens, 241-token prefix x16 layers, 10 Euler steps "
                                "x16 expert layers)", "global_batch": B, "chunk": cfg.chunk,
                    "parallelism": "single GPU"},
+        "output_check": check,
         "latency_bs1": lat,
+        "configs_bs1": configs,
         "tflops_end_to_end": round(flops / (ms_step * 1e-3) / 1e12, 1),
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -275,10 +275,12 @@ int svla_action_out_euler(const void* a, int lda, const void* w, int ldw, float*
  * attention -> O + residual -> RMSNorm -> gate|up + SiLU*up -> down +
  * residual), the final RMSNorm + action_out and x <- x + dt * v -- in ONE
  * persistent launch for small batches (batch * chunk rows; chunk <= 64).
- * Same arithmetic and rounding points as the layer-by-layer entry points
- * (svla_linear_*_bf16, svla_attention_bf16, svla_action_out_euler), except
- * that the attention softmax is normalised before its probabilities are
- * rounded to bf16, as the reference torch module does.  Replaces
+ * Rounding points of the reference torch modules: each RMSNorm output is
+ * rounded once, bf16(x * (1/rms) * gain), before its projection (the
+ * layer-by-layer GEMMs instead round bf16(x * gain) and scale by 1/rms in
+ * their epilogue), projections round to bf16, RoPE runs in fp32 on the bf16
+ * projection, the attention softmax is normalised before its probabilities
+ * are rounded to bf16, residual adds round to bf16.  Replaces
  * action_expert_self_forward / action_expert_cross_forward
  * (vla/action_expert_bf16.py:662-803) as driven by joint_transformer
  * (vla/vla.py:194-212) and postprocessing (vla/vla.py:218-222), plus the
@@ -330,6 +332,10 @@ typedef struct svla_expert_plan {
   int grid;
   int team_xcd;
   int team_size;
+  int spin_limit; /* polls before a wait gives up (svla_expert_prepare: 1 << 22,
+                     about seconds); a caller may lower it, e.g. to exercise
+                     the failure path: status 1 and NaN actions, every
+                     workgroup still exits */
 } svla_expert_plan;
 
 /* Device workspace bytes svla_expert_prepare needs for d (phase table,
@@ -354,8 +360,22 @@ int svla_expert_prepare(const svla_expert_desc* d, void* ws, long ws_bytes, int 
 int svla_expert_run(const svla_expert_plan* plan, svla_stream_t stream);
 
 /* Status word of the last run (synchronous copy): 0 ok, 1 a wait gave up,
- * 2 the XCD team could not form. */
+ * 2 the XCD team could not form.  A run that gave up also fills x_out with
+ * NaN, so a caller that replays a graph without reading the status still
+ * sees the failure. */
 int svla_expert_status(const svla_expert_plan* plan, int* status);
+
+/* Byte offset, inside the workspace laid out for d, of the activation that
+ * enters expert layer `layer` (0..n_layers-1) at Euler step `step`;
+ * layer == n_layers: the last layer's output (the input of the final norm
+ * and action projection).  Each such buffer is written once per run and
+ * keeps its value until the next run, so a caller can read every layer's
+ * output of every step back after svla_expert_run -- the per-layer check of
+ * the reference's layer tests (vla/action_expert_bf16.py:848-906).  Layout:
+ * fragment-major bf16 [64 rows][hidden]: element (m, k) at
+ * ((((k/32)*4 + m/16)*64 + m%16 + 16*((k/8)%4))*8 + k%8).  -1 if d, step or
+ * layer is invalid. */
+long svla_expert_trace_offset(const svla_expert_desc* d, int step, int layer);
 
 /* ------------------------------------------------------------ attention --
  * Fused GQA attention: O = softmax(scale * Q K^T + mask) V per head, query

@@ -99,3 +99,50 @@ def test_strict_forced_tile_without_kernel_is_einval(tile, norm, rope):
         lib.svla_gemm_set_tile(-1)
     assert rc == -22
     assert lib.svla_gemm_set_tile(20 | 0x100) == -22
+
+
+def _fake_expert_desc(cfg):
+    """An expert descriptor with placeholder (never dereferenced) addresses:
+    the plan and the trace offsets are computed on the host alone."""
+    from smolvla import _lib
+    e = cfg.expert
+    layers = (_lib.ExpertLayer * cfg.expert_layers)()
+    for i in range(cfg.expert_layers):
+        L = layers[i]
+        L.cross = int(cfg.is_cross(i))
+        L.w_qkv = L.w_o = L.w_gu = L.w_down = L.norm1 = L.norm2 = 0x10000
+        if L.cross:
+            L.cross_k = L.cross_v = 0x10000
+    d = _lib.ExpertDesc()
+    d.batch, d.chunk, d.hidden = 1, cfg.chunk, e.hidden
+    d.n_q_heads, d.n_kv_heads, d.head_dim, d.inter = e.n_q_heads, e.n_kv_heads, 64, e.inter
+    d.action_dim, d.n_layers, d.prefix_len = cfg.action_dim, cfg.expert_layers, cfg.prefix_len
+    d.num_steps, d.ld_cross, d.rms_eps, d.dt = cfg.num_steps, 2 * e.kv_dim, 1e-5, -0.1
+    for f in ("w_action_in", "b_action_in", "w_time_in_a", "time_bias", "w_time_out",
+              "b_time_out", "norm_out", "w_action_out", "rope_cos", "rope_sin", "x_in", "x_out"):
+        setattr(d, f, 0x10000)
+    d.layers = layers
+    return d, layers
+
+
+def test_expert_trace_offsets_host_only():
+    """svla_expert_trace_offset: one distinct, 256-byte aligned buffer per
+    layer boundary of every Euler step, inside the workspace, in step order;
+    -1 past the ends."""
+    from smolvla import _lib
+    from smolvla.config import SmolVLAConfig
+    cfg = SmolVLAConfig()
+    d, _keep = _fake_expert_desc(cfg)
+    lib = _lib.load()
+    size = lib.svla_expert_workspace_size(ctypes.byref(d))
+    assert size > 0
+    buf = ((cfg.expert.hidden + 31) // 32) * 4096
+    offs = [lib.svla_expert_trace_offset(ctypes.byref(d), s, l)
+            for s in range(cfg.num_steps) for l in range(cfg.expert_layers + 1)]
+    assert all(o >= 0 and o % 256 == 0 and o + buf <= size for o in offs)
+    assert offs == sorted(offs) and len(set(offs)) == len(offs)
+    assert all(b - a >= buf for a, b in zip(offs, offs[1:]))
+    for s, l in ((-1, 0), (cfg.num_steps, 0), (0, -1), (0, cfg.expert_layers + 1)):
+        assert lib.svla_expert_trace_offset(ctypes.byref(d), s, l) == -1
+    d.head_dim = 32                                      # unsupported: invalid descriptor
+    assert lib.svla_expert_trace_offset(ctypes.byref(d), 0, 0) == -1

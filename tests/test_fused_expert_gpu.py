@@ -19,6 +19,14 @@ from smolvla.params import smolvla_inputs, smolvla_params
 pytestmark = pytest.mark.gpu
 ACTION_ATOL = 5e-2
 ENGINE_ATOL = 2e-2
+LAYER_RTOL = 1e-2      # north star: max relative error per layer output
+CHAIN_RTOL = 3e-2      # 16 stacked layers from the oracle's own step input (as for the stacks)
+
+
+def _rel(got, want):
+    """max |got - want| / max |want| in fp32."""
+    got, want = got.float(), want.float()
+    return ((got - want).abs().max() / want.abs().max()).item()
 
 
 def _engine(cfg, P, batch, **kw):
@@ -87,3 +95,104 @@ def test_fused_expert_one_xcd_team_matches(full1):
     b = eng.run(*dev).cpu()
     assert eng.fx.status() == 0
     assert torch.equal(a, b)
+
+
+def test_full_config_fused_expert_per_layer(full1):
+    """Every layer of the fused expert (the batch-1 default path) against the
+    oracle's layer on the same input: the fused launch's per-layer outputs
+    are read back from its workspace (``svla_expert_trace_offset``), as the
+    reference checks each expert layer on its own
+    (vla/action_expert_bf16.py:848-906).  Steps 0 and 9; plus the step-0
+    expert input against the oracle's action/time embedding, and the 16
+    layers chained from the oracle's own step-0 input."""
+    cfg, P, inputs, _ = full1
+    dev = [t.cuda() for t in inputs]
+    eng = _engine(cfg, P, 1)
+    print("full config batch 1: fused expert, per layer", flush=True)
+    eng.run(*dev)
+    e, L, Lc = cfg.expert, cfg.chunk, cfg.prefix_len
+    ckv = {i: (ck.cpu().reshape(1, Lc, -1), cv.cpu().reshape(1, Lc, -1))
+           for i, (ck, cv) in eng.cross.items()}
+    worst = 0.0
+    with torch.inference_mode():
+        for step in (0, cfg.num_steps - 1):
+            for li in range(cfg.expert_layers):
+                x = eng.fx.trace(step, li).cpu().view(1, L, e.hidden)
+                got = eng.fx.trace(step, li + 1).cpu().view(1, L, e.hidden)
+                lp = P["expert"][li]
+                if cfg.is_cross(li):
+                    want = ref._cross_with_projected(x, *ckv[li], lp, e)
+                else:
+                    want = ref.expert_self_block(x, lp, e)
+                err = _rel(got, want)
+                worst = max(worst, err)
+                assert err <= LAYER_RTOL, f"step {step} layer {li}: {err:.3e}"
+        # step 0's expert input: action_in / time MLP of the noise at t = 1
+        h0 = ref.expert_input(inputs[3].float(), 1.0, P, cfg)
+        e_in = _rel(eng.fx.trace(0, 0).cpu().view(1, L, e.hidden), h0)
+        assert e_in <= LAYER_RTOL, e_in
+        # the oracle's own chain from its step-0 input
+        h = h0
+        for li in range(cfg.expert_layers):
+            lp = P["expert"][li]
+            h = (ref._cross_with_projected(h, *ckv[li], lp, e) if cfg.is_cross(li)
+                 else ref.expert_self_block(h, lp, e))
+            e_ch = _rel(eng.fx.trace(0, li + 1).cpu().view(1, L, e.hidden), h)
+            assert e_ch <= CHAIN_RTOL, f"chain layer {li}: {e_ch:.3e}"
+    print(f"fused expert per layer: worst {worst:.3e}, input {e_in:.3e}, chain end {e_ch:.3e}")
+
+
+def test_run_raises_on_expert_status():
+    """A non-zero status word makes the engine raise (the word planted from
+    the host into the workspace after a good run; no kernel is made to fail)."""
+    cfg = small_config()
+    P = smolvla_params(cfg, seed=31, norm_init="random")
+    dev = [t.cuda() for t in smolvla_inputs(cfg, batch=1, seed=32)]
+    eng = _engine(cfg, P, 1, fused_expert=True)
+    eng.run(*dev)
+    eng.check()
+    fx = eng.fx
+    off = fx.plan.status - fx.workspace.data_ptr()
+    fx.workspace[off:off + 4].copy_(torch.tensor([1, 0, 0, 0], dtype=torch.uint8))
+    torch.cuda.synchronize()
+    with pytest.raises(RuntimeError, match="status 1"):
+        eng.check()
+    real = fx.status
+    fx.status = lambda: 2                      # a run() whose expert reports a team failure
+    try:
+        with pytest.raises(RuntimeError, match="status 2"):
+            eng.run(*dev)
+    finally:
+        fx.status = real
+    eng.run(*dev)                              # the next good run clears the word
+    assert fx.status() == 0
+
+
+def test_expert_gives_up_loudly_with_a_tiny_spin_limit():
+    """The failure path itself, forced from the host: with a spin limit of
+    one poll, some phase wait gives up; every workgroup still leaves (the
+    launch returns), the status word reads 1 and the actions are NaN.  A
+    later run with the normal limit is correct again."""
+    cfg = small_config()
+    P = smolvla_params(cfg, seed=31, norm_init="random")
+    dev = [t.cuda() for t in smolvla_inputs(cfg, batch=1, seed=32)]
+    eng = _engine(cfg, P, 1, fused_expert=True, use_graph=False)
+    good = eng.run(*dev).cpu()
+    fx = eng.fx
+    limit = fx.plan.spin_limit
+    assert limit > 1000
+    fx.plan.spin_limit = 1
+    print("fused expert with spin limit 1 (forced give-up)", flush=True)
+    try:
+        eng.load_inputs(*dev)
+        eng.step()
+        torch.cuda.synchronize()
+        bad = eng.x_t.cpu()
+        assert fx.status() == 1
+        assert torch.isnan(bad).all()
+        with pytest.raises(RuntimeError, match="status 1"):
+            eng.check()
+    finally:
+        fx.plan.spin_limit = limit
+    again = eng.run(*dev).cpu()
+    assert torch.equal(again, good)

@@ -43,11 +43,13 @@
 //    holds its k-range of the 64 activation rows in registers and streams
 //    its 16x16x32 MFMA weight fragments into a private LDS region by LDS-DMA
 //    (no registers held while they fly); the partial tiles meet in LDS.
-//    The RMSNorm in front of a projection is fused: the gain multiplies the
-//    unit's weight fragments (16 rows of W, where the activations are 64
-//    rows) on the way into the MFMAs, row sums of squares come from the
-//    activation fragments, 1/rms is applied in the epilogue.  Paired epilogues (RoPE pairs (d, d+32), SiLU(gate) * up) use
-//    the 16-column tile of 8 columns + their partners.  The V columns of a
+//    The RMSNorm in front of a projection is fused: the row sums of squares
+//    come from the activation fragments and meet in LDS, then every wave
+//    turns its fragments into bf16(x * (1/rms) * gain) before the MFMAs --
+//    the single rounding of torch's bf16 RMSNorm, so each layer output
+//    follows the reference module's rounding points.  Paired epilogues
+//    (RoPE pairs (d, d+32), SiLU(gate) * up) use the 16-column tile of 8
+//    columns + their partners.  The V columns of a
 //    self layer's QKV projection are written transposed (V^T [kv][64 keys])
 //    for the attention.
 //  * Attention units: one (sample, head); K, V^T and the queries are staged
@@ -58,9 +60,10 @@
 //    (vla/text_encoder_bf16.py:117-126).  The P.V operand is V^T straight
 //    from global memory (the cross layers' V is transposed by the launch's
 //    first phase).
-//  * Every wait is bounded: past kSpin polls (or when another workgroup has
-//    already given up) the workgroup sets the status word and leaves, so the
-//    grid always drains.  The team is either every workgroup of the launch
+//  * Every wait is bounded: past the plan's spin limit (kSpin polls unless
+//    the caller lowers it) or when another workgroup has already given up,
+//    the workgroup sets the status word, fills the action output with NaN
+//    and leaves, so the grid always drains and a failed chunk is loud.  The team is either every workgroup of the launch
 //    or, optionally, the workgroups of one XCD (selected by the hardware
 //    XCC_ID register); the write-through / write-once discipline keeps the
 //    results correct whichever CUs take part.
@@ -111,12 +114,15 @@ struct XPhase {
   const float* sin_t;
   int rope_cols, rope_period;
   bf16* vt;     // ROPE: columns >= rope_cols go here transposed, [sample][col][XVTS]
+  bf16* c_lo;   // ROPE: the bf16 remainder o - bf16(o) of every rotated column (same layout as c)
   int chunk;    // rows per sample (ROPE V^T, attention queries)
   const float* x_in;  // Euler: x_out[m, n] = x_in[m, n] + dt * bf16(v) (fp32, leading dim N)
   float* x_out;
   float dt;
   // attention: unit = sample * heads + head; V given transposed
   const bf16* q;
+  const bf16* q_lo;  // remainder of the fp32 RoPE output: Q = q + q_lo to ~16 bits
+  const bf16* k_lo;  // the same for K (self layers; null: K is plain bf16)
   const bf16* k;
   const bf16* vt_in;
   bf16* o;
@@ -145,6 +151,7 @@ struct XArgs {
   unsigned* status;  // XStat of the launch (0 = ok)
   int team_xcd;      // < 0: every workgroup; else the workgroups on this XCD
   int team_size;     // participants expected when team_xcd >= 0
+  int spin;          // polls before a wait gives up
 };
 
 // Loads through pointers read from the phase table: tell the compiler they
@@ -222,7 +229,7 @@ __device__ bool wait_phase(const XArgs& g, int row, unsigned target) {
     const unsigned st = __shfl(v, kSub, 64);
     if (__builtin_amdgcn_readfirstlane(s) >= target) return true;
     if (__builtin_amdgcn_readfirstlane(st) != 0u) return false;
-    if (n >= kSpin) {
+    if (n >= g.spin) {
       if (lane == 0)
         __hip_atomic_store(g.status, (unsigned)XS_TIMEOUT, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -371,8 +378,8 @@ __device__ __forceinline__ void load_x(CPhase& P, GemmRegs& r, int t0, int t1) {
 #pragma unroll
   for (int tm = 0; tm < 4; ++tm) r.ss[tm] = 0.f;
   if (P.norm_w) {
-    // per-row sums of squares (the gains go onto the weight fragments in
-    // gemm_mma: 16 rows of W per unit instead of 64 of A); the activations
+    // per-row sums of squares of the raw activations (norm_x applies
+    // 1 / rms and the gains once the waves' sums have met); the activations
     // landed first
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(wc_vm(0));
@@ -446,7 +453,6 @@ union XShared {
   struct {
     float part[XW][XBM * XPS];  // partial tiles of the waves
     float ss[XW][XBM];          // per-wave row sums of squares
-    float rs[XBM];              // row scale 1 / rms
     bf16 gain[XW][512];         // norm gains of each wave's k range (staged)
   } g;
   struct {
@@ -454,8 +460,47 @@ union XShared {
     float asum[XW][16];
     float o[XW][64][16];        // partial O^T [key group][d][query]
     bf16 q[64 * 64];            // staged queries (rows swizzled as K)
+    bf16 q_lo[64 * 64];         // their bf16 remainders (when P.q_lo)
   } a;
 };
+
+// Fused RMSNorm of a unit's activations, once the per-wave row sums of
+// squares are in LDS: every element of the wave's fragments becomes
+// bf16((x * (1 / rms)) * gain) in fp32 -- the single rounding of torch's bf16
+// RMSNorm (the reference module's nn.RMSNorm, vla/action_expert_bf16.py:74-78),
+// with 1 / rms = 1 / sqrt(sum / K + eps) and the waves' sums added in wave
+// order.  The gains of the wave's k range were staged in LDS by dma_gain
+// (landed: load_x waited for every load of the wave).  Rows past M are zero
+// and stay zero.
+__device__ __forceinline__ void norm_x(CPhase& P, GemmRegs& r, const XShared& sh, int t0,
+                                       int t1) {
+  const int lane = tidx() & 63, wave = wave_id();
+  const int fr = lane & 15, G = lane >> 4;
+  int ks0, kcnt;
+  wave_krange(P.K, wave, ks0, kcnt);
+  float rs[4];
+#pragma unroll
+  for (int tm = 0; tm < 4; ++tm) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < XW; ++w) t += sh.g.ss[w][tm * 16 + fr];
+    rs[tm] = 1.0f / sqrtf(t / (float)P.K + P.norm_eps);
+  }
+  const bf16* gain = sh.g.gain[wave];
+#pragma unroll
+  for (int j = 0; j < XKS; ++j) {
+    if (j >= kcnt) break;  // wave-uniform
+    const bf16x8 gv = *reinterpret_cast<const bf16x8*>(gain + j * 32 + G * 8);
+#pragma unroll
+    for (int tm = 0; tm < 4; ++tm) {
+      if (tm < t0 || tm >= t1) continue;  // wave-uniform
+      bf16x8 x = r.fx[j][tm];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = f2bf(__fmul_rn(__fmul_rn(bf2f(x[e]), rs[tm]), bf2f(gv[e])));
+      r.fx[j][tm] = x;
+    }
+  }
+}
 
 __device__ __forceinline__ f32x4 sum_parts(const XShared& sh, int ml, int nl) {
   f32x4 t = *reinterpret_cast<const f32x4*>(&sh.g.part[0][ml * XPS + nl]);
@@ -470,11 +515,10 @@ __device__ void gemm_epilogue(CPhase& P, const EpiItem& it, const EpiPre& e,
                               const XShared& sh) {
   if (!it.on) return;
   const int m = it.ml, n = it.n;
-  const float sc = P.norm_w ? sh.g.rs[m] : 1.0f;
   auto get = [&](int nl, float v[4]) {
     const f32x4 t = sum_parts(sh, m, nl);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = t[i] * sc;
+    for (int i = 0; i < 4; ++i) v[i] = t[i];
   };
   if (P.epi == XE_STORE) {
     float v[4];
@@ -508,6 +552,20 @@ __device__ void gemm_epilogue(CPhase& P, const EpiItem& it, const EpiPre& e,
     bf16* crow = static_cast<bf16*>(P.c) + (long)m * P.ldc;
     st4_wt(crow + n, o1);
     st4_wt(crow + n + 32, o2);
+    if (P.c_lo) {
+      // the reference scores the fp32 RoPE output (vla/text_encoder_bf16.py:
+      // 92-104, 117-122): keep what bf16 drops (exact in fp32), so that the
+      // attention takes Q . K^T with Q = hi + lo
+      float l1[4], l2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        l1[i] = __fsub_rn(o1[i], rbf(o1[i]));
+        l2[i] = __fsub_rn(o2[i], rbf(o2[i]));
+      }
+      bf16* lrow = P.c_lo + (long)m * P.ldc;
+      st4_wt(lrow + n, l1);
+      st4_wt(lrow + n + 32, l2);
+    }
   } else if (P.epi == XE_SILU) {
     // bf16(silu(bf16(gate))) * bf16(up), output column (n / 64) * 32 + n % 64
     // (vla/text_encoder_bf16.py:130-131)
@@ -542,7 +600,7 @@ __device__ __forceinline__ void vt_item(CPhase& P, int ct, const XShared& sh, in
       const int ml = b * P.chunk + key;
 #pragma unroll
       for (int w = 0; w < XW; ++w) t += sh.g.part[w][ml * XPS + c];
-      t = rbf(t * (P.norm_w ? sh.g.rs[ml] : 1.0f));
+      t = rbf(t);
     }
     v[i] = t;
   }
@@ -565,10 +623,8 @@ __device__ void vt_epilogue(CPhase& P, int ct, const XShared& sh, int t0, int t1
 }
 
 
-// gain: the norm gains of the wave's k range (LDS), or null: the weight
-// fragment is multiplied by them (rounded to bf16) before the MFMA
 __device__ __forceinline__ void gemm_mma(CPhase& P, const GemmRegs& r, const bf16* sw,
-                                         const bf16* gain, f32x4 (&acc)[4], int t0, int t1) {
+                                         f32x4 (&acc)[4], int t0, int t1) {
   const int lane = tidx() & 63, wave = wave_id();
   const int fr = lane & 15, G = lane >> 4;
   int ks0, kcnt;
@@ -576,12 +632,7 @@ __device__ __forceinline__ void gemm_mma(CPhase& P, const GemmRegs& r, const bf1
 #pragma unroll
   for (int j = 0; j < XKS; ++j) {
     if (j >= kcnt) break;  // wave-uniform
-    bf16x8 fw = *reinterpret_cast<const bf16x8*>(sw + j * XWSTEP + fr * 32 + wswz(fr, G) * 8);
-    if (gain) {  // uniform
-      const bf16x8 gv = *reinterpret_cast<const bf16x8*>(gain + j * 32 + G * 8);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) fw[e] = f2bf(__fmul_rn(bf2f(fw[e]), bf2f(gv[e])));
-    }
+    const bf16x8 fw = *reinterpret_cast<const bf16x8*>(sw + j * XWSTEP + fr * 32 + wswz(fr, G) * 8);
 #pragma unroll
     for (int tm = 0; tm < 4; ++tm)
       if (tm >= t0 && tm < t1)  // wave-uniform
@@ -617,6 +668,7 @@ __device__ __forceinline__ int vswz(int d, int c, int ldvt) {
   return ldvt <= 64 ? rswz8(d, c) : c ^ (d & 15);
 }
 constexpr int kAttnVt = XMAXK * 64;  // V^T offset in the staging region (bf16)
+constexpr int kAttnKlo = XKW * 64;   // K remainders (at most XKW keys: self layers) (bf16)
 
 // K (keys clamped to Lk - 1) and V^T (64 rows of ldvt keys; the writers zero
 // the keys past Lk) of sample b, kv head g: 1 KB per DMA instruction, the
@@ -631,6 +683,15 @@ __device__ __forceinline__ void attn_stage_kv(CPhase& P, int b, int g, bf16* st)
     __builtin_amdgcn_global_load_lds((void*)(kb + (unsigned)min(key, P.lk - 1) * (unsigned)P.ldk + c * 8),
                                      (lds_ptr_t)(st + i * 512), 16, 0, 0);
   }
+  if (P.k_lo && P.lk <= XKW) {  // uniform; rows XKW.. of the K region are free then
+    const bf16* kl = P.k_lo + b * P.k_bs + g * 64;
+    for (int i = wave; i < nki; i += XW) {
+      const int key = i * 8 + (lane >> 3);
+      const int c = rswz8(key, lane & 7);
+      __builtin_amdgcn_global_load_lds((void*)(kl + (unsigned)min(key, P.lk - 1) * (unsigned)P.ldk + c * 8),
+                                       (lds_ptr_t)(st + kAttnKlo + i * 512), 16, 0, 0);
+    }
+  }
   const bf16* vb = P.vt_in + b * P.vt_bs + (long)g * 64 * P.ldvt;
   const int lg = 31 - __builtin_clz(P.ldvt);  // ldvt is 64, 128 or 256
   const int nvi = P.ldvt >> 3;                // 64 ldvt elements / 512 per instruction
@@ -643,14 +704,18 @@ __device__ __forceinline__ void attn_stage_kv(CPhase& P, int b, int g, bf16* st)
 }
 // query rows r0 .. r0 + 8 n - 1 (clamped to chunk - 1) of sample b, head h
 // into LDS rows 0 .. 8 n - 1: one instruction for each of waves 0 .. n - 1
-__device__ __forceinline__ void attn_stage_q(CPhase& P, int b, int h, int r0, int n, bf16* lq) {
+__device__ __forceinline__ void attn_stage_q(CPhase& P, int b, int h, int r0, int n, bf16* lq,
+                                             bf16* lq_lo) {
   const int lane = tidx() & 63, wave = wave_id();
   if (wave >= n) return;  // wave-uniform
-  const bf16* qb = P.q + b * P.q_bs + h * 64;
   const int row = wave * 8 + (lane >> 3);
   const int c = rswz8(row, lane & 7);
-  __builtin_amdgcn_global_load_lds((void*)(qb + (unsigned)min(r0 + row, P.chunk - 1) * (unsigned)P.ldq + c * 8),
-                                   (lds_ptr_t)(lq + wave * 512), 16, 0, 0);
+  const unsigned off = (unsigned)(b * P.q_bs + h * 64) +
+                       (unsigned)min(r0 + row, P.chunk - 1) * (unsigned)P.ldq + c * 8;
+  __builtin_amdgcn_global_load_lds((void*)(P.q + off), (lds_ptr_t)(lq + wave * 512), 16, 0, 0);
+  if (P.q_lo)  // uniform
+    __builtin_amdgcn_global_load_lds((void*)(P.q_lo + off), (lds_ptr_t)(lq_lo + wave * 512), 16,
+                                     0, 0);
 }
 __device__ __forceinline__ void attn_decode(CPhase& P, int unit, int& b, int& h, int& qt) {
   const int bh = unit / P.q_tiles;
@@ -675,10 +740,12 @@ __device__ __forceinline__ void attn_solo(CPhase& P, int b, int h, int qt, int l
   const int Lq = P.chunk, Lk = P.lk, ldvt = P.ldvt;
   const int nkt = (Lk + 15) / 16;  // <= KT (uniform)
   const int r = qt * 16 + col, qc = min(r, Lq - 1);
-  bf16x8 qf[2];
+  bf16x8 qf[2], ql[2];
 #pragma unroll
-  for (int ds = 0; ds < 2; ++ds)
+  for (int ds = 0; ds < 2; ++ds) {
     qf[ds] = *reinterpret_cast<const bf16x8*>(sh.a.q + r * 64 + rswz8(r, ds * 4 + G) * 8);
+    if (P.q_lo) ql[ds] = *reinterpret_cast<const bf16x8*>(sh.a.q_lo + r * 64 + rswz8(r, ds * 4 + G) * 8);
+  }
   f32x4 s[KT];
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
@@ -687,7 +754,14 @@ __device__ __forceinline__ void attn_solo(CPhase& P, int b, int h, int qt, int l
     const int key = t * 16 + col;
 #pragma unroll
     for (int ds = 0; ds < 2; ++ds) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(lk + key * 64 + rswz8(key, ds * 4 + G) * 8);
+      const int o = key * 64 + rswz8(key, ds * 4 + G) * 8;
+      const bf16x8 kf = *reinterpret_cast<const bf16x8*>(lk + o);
+      if (P.k_lo) {  // uniform: K = hi + lo
+        const bf16x8 kl = *reinterpret_cast<const bf16x8*>(lk + kAttnKlo + o);
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qf[ds], s[t], 0, 0, 0);
+      }
+      if (P.q_lo)  // uniform: Q = hi + lo
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, ql[ds], s[t], 0, 0, 0);
       s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ds], s[t], 0, 0, 0);
     }
   }
@@ -759,8 +833,8 @@ __device__ void attn_unit(CPhase& P, int unit, XShared& sh, bf16* st, bool kv_st
   const int Lq = P.chunk, Lk = P.lk, ldvt = P.ldvt;
   const bool solo = Lk <= XKW;  // uniform
   if (!kv_staged) attn_unit_kv(P, unit, st);
-  if (solo) attn_stage_q(P, b, h, 0, 8, sh.a.q);
-  else attn_stage_q(P, b, h, qt * 16, 2, sh.a.q);
+  if (solo) attn_stage_q(P, b, h, 0, 8, sh.a.q, sh.a.q_lo);
+  else attn_stage_q(P, b, h, qt * 16, 2, sh.a.q, sh.a.q_lo);
   // every wave's DMA landed, then the staged rows are visible to all
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
   __builtin_amdgcn_s_waitcnt(wc_vm(0));
@@ -777,11 +851,14 @@ __device__ void attn_unit(CPhase& P, int unit, XShared& sh, bf16* st, bool kv_st
   const int k0 = wave * XKG;
   const int nkt = min(KT, max(0, (Lk - k0 + 15) / 16));  // key tiles with keys (uniform)
   const int qc = min(qt * 16 + col, Lq - 1);
-  bf16x8 qf[2];
+  bf16x8 qf[2], ql[2];
 #pragma unroll
-  for (int ds = 0; ds < 2; ++ds)
+  for (int ds = 0; ds < 2; ++ds) {
     qf[ds] = *reinterpret_cast<const bf16x8*>(sh.a.q + col * 64 + rswz8(col, ds * 4 + G) * 8);
+    if (P.q_lo) ql[ds] = *reinterpret_cast<const bf16x8*>(sh.a.q_lo + col * 64 + rswz8(col, ds * 4 + G) * 8);
+  }
   // S^T tiles: s[t] lane holds scores of keys k0 + 16 t + 4 G + i, query col
+  // (K remainders exist only up to XKW keys, the one-wave path: not here)
   f32x4 s[KT];
 #pragma unroll
   for (int t = 0; t < KT; ++t) {
@@ -791,6 +868,8 @@ __device__ void attn_unit(CPhase& P, int unit, XShared& sh, bf16* st, bool kv_st
 #pragma unroll
     for (int ds = 0; ds < 2; ++ds) {
       const bf16x8 kf = *reinterpret_cast<const bf16x8*>(lk + key * 64 + rswz8(key, ds * 4 + G) * 8);
+      if (P.q_lo)  // uniform: Q = hi + lo
+        s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, ql[ds], s[t], 0, 0, 0);
       s[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ds], s[t], 0, 0, 0);
     }
   }
@@ -923,6 +1002,44 @@ __device__ __forceinline__ unsigned touch_phase(CPhase* ph) {
   return t;
 }
 
+// A workgroup that leaves because the launch gave up (a wait timed out, the
+// team did not form) fills the action output (the last phase's Euler state)
+// with NaN: a caller that never reads the status word -- a replayed graph,
+// for one -- still gets an unmistakable result.  (A give-up also sets the
+// status word, so such a chunk is reported failed whichever of its Euler
+// units still wrote.)
+__device__ void poison_actions(const XArgs& g) {
+  CPhase& L = g.ph[g.n_ph - 1];
+  if (L.kind != XK_GEMM || L.epi != XE_EULER || !L.x_out) return;  // uniform
+  const int n2 = L.M * L.N / 2;  // N even (action_dim % 16 == 0)
+  const float q = __builtin_nanf("");
+  for (int i = tidx(); i < n2; i += XT) st2f_wt(L.x_out + 2 * i, q, q);
+  __builtin_amdgcn_s_waitcnt(wc_vm(0));
+}
+
+// One-XCD team mode: workgroup 0, when it is not a member, watches that the
+// team forms (enough workgroups landed on the team's XCD); if it does not
+// within the spin limit, it sets XS_TEAM and poisons the output.
+__device__ void team_watch(const XArgs& g) {
+  __shared__ int s_fail;
+  if (wave_id() == 0) {
+    const unsigned* reg = g.cnt + (size_t)g.n_ph * kSub * kCntStride;
+    bool fail = true;
+    for (int n = 0; n < g.spin; ++n) {
+      if (__builtin_amdgcn_readfirstlane(ld_agent(reg)) >= (unsigned)g.team_size ||
+          __builtin_amdgcn_readfirstlane(ld_agent(g.status)) != 0u) {
+        fail = false;  // formed, or a member already reported a failure
+        break;
+      }
+    }
+    if (fail && (tidx() & 63) == 0)
+      __hip_atomic_store(g.status, (unsigned)XS_TEAM, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if ((tidx() & 63) == 0) s_fail = fail;
+  }
+  __syncthreads();
+  if (s_fail) poison_actions(g);
+}
+
 __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
   __shared__ XShared sh;
   __shared__ __attribute__((aligned(1024))) bf16 s_w[XW][XKS * XWSTEP];  // per-wave weights
@@ -946,14 +1063,18 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
   }
   __syncthreads();
   const int rank = s_rank;
-  if (rank < 0) return;
+  if (rank < 0) {
+    if (g.team_xcd >= 0 && blockIdx.x == 0) team_watch(g);
+    return;
+  }
   const int team = g.team_xcd >= 0 ? g.team_size : (int)gridDim.x;
+  bool failed = false;  // this workgroup gave up (poisons the output on its way out)
   if (g.team_xcd >= 0) {
     if (wave == 0) {
       // every member registered before anyone relies on the team's size
       const unsigned* reg = g.cnt + (size_t)g.n_ph * kSub * kCntStride;
       bool ok = false;
-      for (int n = 0; n < kSpin; ++n) {
+      for (int n = 0; n < g.spin; ++n) {
         const unsigned rr = __builtin_amdgcn_readfirstlane(ld_agent(reg));
         if (rr >= (unsigned)team) { ok = true; break; }
         if (__builtin_amdgcn_readfirstlane(ld_agent(g.status)) != 0u) break;
@@ -963,14 +1084,14 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
       if (lane == 0) s_rank = ok ? rank : -1;
     }
     __syncthreads();
-    if (s_rank < 0) return;
+    failed = s_rank < 0;
   }
 
   if (wave == 1) {
     const unsigned t = touch_phase(g.ph) ^ (g.n_ph > 1 ? touch_phase(g.ph + 1) : 0u);
     asm volatile("" ::"s"(t));
   }
-  for (int p = 0; p < g.n_ph; ++p) {
+  for (int p = 0; p < g.n_ph && !failed; ++p) {
     CPhase& P = g.ph[p];
     if (rank >= P.units) continue;
     const int tid = tidx(), lane = tid & 63;  // (not hoisted: see tidx)
@@ -997,7 +1118,10 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
         if (lane == 0) s_rank = ok ? rank : -1;
       }
       __syncthreads();
-      if (s_rank < 0) return;
+      if (s_rank < 0) {
+        failed = true;
+        break;
+      }
     }
     if (P.kind == XK_GEMM) {
       for (int j = 0; j < mine; ++j) {
@@ -1013,13 +1137,16 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
         if (load) {
           load_x(P, r, t0, t1);
           if (P.norm_w) {
-            // per-row sums of squares of the whole K range meet in LDS
+            // per-row sums of squares of the whole K range meet in LDS, then
+            // every wave normalises its activation fragments
 #pragma unroll
             for (int tm = 0; tm < 4; ++tm) {
               float t = r.ss[tm];
               t = xor32_sum(xor16_sum(t));
               if (lane < 16) sh.g.ss[wave][tm * 16 + lane] = t;
             }
+            wg_sync_lds();
+            norm_x(P, r, sh, t0, t1);
           }
         }
         f32x4 acc[4];
@@ -1029,21 +1156,12 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         __builtin_amdgcn_s_waitcnt(wc_vm(0));
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        gemm_mma(P, r, sw, P.norm_w ? sh.g.gain[wave] : nullptr, acc, t0, t1);
+        gemm_mma(P, r, sw, acc, t0, t1);
         put_partial(acc, sh);
         wg_sync_lds();  // also: this wave's weight reads are done
         // the next unit's weights stream in during this unit's epilogue
         if (j + 1 < mine)
           dma_w(P.epi, P.w, P.N, P.K, P.ldw, (u + team) % P.col_tiles, sw);
-        if (load && P.norm_w) {
-          if (tid < XBM) {
-            float t = 0.f;
-#pragma unroll
-            for (int w = 0; w < XW; ++w) t += sh.g.ss[w][tid];
-            sh.g.rs[tid] = 1.0f / sqrtf(t / (float)P.K + P.norm_eps);
-          }
-          wg_sync_lds();
-        }
         if (vt) vt_epilogue(P, ct, sh, t0, t1);
         else gemm_epilogue(P, it, e, sh);
         wg_sync_lds();  // partial tiles free for the next unit
@@ -1063,6 +1181,7 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
       __hip_atomic_fetch_add(g.cnt + ((size_t)p * kSub + (rank & (kSub - 1))) * kCntStride,
                              (unsigned)mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  if (failed) poison_actions(g);
 }
 
 __global__ void clear_u32_kernel(unsigned* p, long n) {
@@ -1120,7 +1239,11 @@ bool desc_ok(const svla_expert_desc* d) {
 }
 
 // Builds the phase list (and, with base != nullptr, the buffer addresses).
-size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, Layout* lay) {
+// trace (optional): the workspace offset of the activation entering each
+// layer of each Euler step, and of the last layer's output: (n_layers + 1)
+// entries per step, step-major.  Fragment-major [64 rows][hidden] bf16.
+size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, Layout* lay,
+             std::vector<size_t>* trace = nullptr) {
   const int M = d->batch * d->chunk, H = d->hidden, qd = d->n_q_heads * 64,
             kvd = d->n_kv_heads * 64, I = d->inter, A = d->action_dim;
   Layout L{};
@@ -1131,9 +1254,10 @@ size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, La
   L.counters = ar.take(L.n_cnt_words * 4);
   L.status = ar.take(4);
   L.arena = ar.off;
+  size_t last = 0;  // offset of the buffer buf() returned last
   auto buf = [&](size_t bytes) -> char* {
-    const size_t o = ar.take(bytes);
-    return base ? base + o : nullptr;
+    last = ar.take(bytes);
+    return base ? base + last : nullptr;
   };
   // fragment-major activation of N columns (64 rows)
   auto fbuf = [&](int N) { return (bf16*)buf((size_t)((N + 31) / 32) * 4096); };
@@ -1187,6 +1311,7 @@ size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, La
     P.act = SVLA_ACT_SILU;
     ph.push_back(P);
     bf16* ex = fbuf(H);
+    if (trace) trace->push_back(last);
     P = gemm(h_t, H, d->w_time_out, H, H, ex, H);
     P.bias = static_cast<const bf16*>(d->b_time_out);
     ph.push_back(P);
@@ -1195,6 +1320,7 @@ size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, La
       const int nq = Ly.cross ? qd : qd + 2 * kvd;  // projected columns
       const int nqk = Ly.cross ? qd : qd + kvd;     // stored row-major (Q | K)
       bf16* qk = (bf16*)buf((size_t)M * nqk * 2);
+      bf16* qk_lo = (bf16*)buf((size_t)M * nqk * 2);  // remainders of the fp32 RoPE output
       bf16* vt = Ly.cross ? nullptr : (bf16*)buf((size_t)d->batch * kvd * XVTS * 2);
       P = gemm(ex, H, Ly.w_qkv, nq, H, qk, nqk);
       P.epi = XE_ROPE;
@@ -1203,6 +1329,7 @@ size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, La
       P.rope_cols = nqk;
       P.rope_period = d->chunk;
       P.vt = vt;
+      P.c_lo = qk_lo;
       ph.push_back(P);
       bf16* att = fbuf(qd);
       XPhase T{};
@@ -1216,6 +1343,7 @@ size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, La
       T.chunk = d->chunk;
       T.scale = 0.125f;
       T.q = qk; T.ldq = nqk; T.q_bs = (long)d->chunk * nqk;
+      T.q_lo = qk_lo;
       if (Ly.cross) {
         T.k = static_cast<const bf16*>(Ly.cross_k); T.ldk = d->ld_cross;
         T.k_bs = (long)d->prefix_len * d->ld_cross;
@@ -1225,6 +1353,7 @@ size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, La
         T.kv_static = 1;
       } else {
         T.k = qk + qd; T.ldk = nqk; T.k_bs = (long)d->chunk * nqk;
+        T.k_lo = qk_lo + qd;  // chunk <= XKW: the one-wave path, which reads it
         T.vt_in = vt; T.ldvt = XVTS; T.vt_bs = (long)kvd * XVTS;
         T.lk = d->chunk;
         T.causal = 1;
@@ -1241,6 +1370,7 @@ size_t build(const svla_expert_desc* d, char* base, std::vector<XPhase>* out, La
       P.norm_w = static_cast<const bf16*>(Ly.norm2);
       ph.push_back(P);
       bf16* ex2 = fbuf(H);
+      if (trace) trace->push_back(last);
       P = gemm(act, I, Ly.w_down, H, I, ex2, H);
       P.res = ex1; P.ldr = H;
       ph.push_back(P);
@@ -1286,6 +1416,15 @@ long svla_expert_workspace_size(const svla_expert_desc* d) {
   return (long)build(d, nullptr, nullptr, nullptr);
 }
 
+long svla_expert_trace_offset(const svla_expert_desc* d, int step, int layer) {
+  if (!desc_ok(d) || step < 0 || step >= d->num_steps || layer < 0 || layer > d->n_layers)
+    return -1;
+  std::vector<size_t> tr;
+  build(d, nullptr, nullptr, nullptr, &tr);
+  const size_t i = (size_t)step * (d->n_layers + 1) + layer;
+  return i < tr.size() ? (long)tr[i] : -1;
+}
+
 int svla_expert_prepare(const svla_expert_desc* d, void* ws, long ws_bytes, int team_xcd,
                         svla_expert_plan* plan, svla_stream_t stream) {
   if (!desc_ok(d) || !ws || !plan || ((uintptr_t)ws % kAlign) || team_xcd > 7) return SVLA_EINVAL;
@@ -1313,6 +1452,9 @@ int svla_expert_prepare(const svla_expert_desc* d, void* ws, long ws_bytes, int 
   if ((e = hipGetDevice(&dev)) != hipSuccess) return (int)e;
   if ((e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev)) != hipSuccess)
     return (int)e;
+  // a one-XCD team is an eighth of the CUs (MI355X: 8 XCDs of 32 CUs); the
+  // kernel's own registration check catches a team that does not form
+  if (team_xcd >= 0 && (cus % 8 || cus < 8)) return SVLA_EINVAL;
   std::memset(plan, 0, sizeof(*plan));
   plan->phases = base + L.phases;
   plan->n_phases = L.n_ph;
@@ -1322,11 +1464,13 @@ int svla_expert_prepare(const svla_expert_desc* d, void* ws, long ws_bytes, int 
   plan->grid = cus;
   plan->team_xcd = team_xcd < 0 ? -1 : team_xcd;
   plan->team_size = team_xcd < 0 ? cus : cus / 8;
+  plan->spin_limit = kSpin;
   return SVLA_OK;
 }
 
 int svla_expert_run(const svla_expert_plan* plan, svla_stream_t stream) {
-  if (!plan || !plan->phases || plan->n_phases <= 0 || plan->grid <= 0) return SVLA_EINVAL;
+  if (!plan || !plan->phases || plan->n_phases <= 0 || plan->grid <= 0 || plan->spin_limit < 0)
+    return SVLA_EINVAL;
   hipStream_t s = (hipStream_t)stream;
   const long words = plan->counter_words + kAlign / 4;  // counters, then the status word
   hipLaunchKernelGGL(clear_u32_kernel, dim3(256), dim3(256), 0, s, plan->counters, words);
@@ -1338,6 +1482,7 @@ int svla_expert_run(const svla_expert_plan* plan, svla_stream_t stream) {
   g.status = plan->status;
   g.team_xcd = plan->team_xcd;
   g.team_size = plan->team_size;
+  g.spin = plan->spin_limit;
   hipLaunchKernelGGL(expert_kernel, dim3(plan->grid), dim3(XT), 0, s, g);
   SVLA_CHECK_LAUNCH();
   return SVLA_OK;

@@ -40,7 +40,8 @@ class ExpertPlan(ctypes.Structure):
     """``svla_expert_plan`` (include/svla.h)."""
     _fields_ = [("phases", _p), ("n_phases", ctypes.c_int), ("counters", _p),
                 ("counter_words", ctypes.c_long), ("status", _p), ("grid", ctypes.c_int),
-                ("team_xcd", ctypes.c_int), ("team_size", ctypes.c_int)]
+                ("team_xcd", ctypes.c_int), ("team_size", ctypes.c_int),
+                ("spin_limit", ctypes.c_int)]
 
 
 # name -> argtypes (all return int, except RESTYPES)
@@ -90,9 +91,11 @@ SIGNATURES = {
                             _p],
     "svla_expert_run": [ctypes.POINTER(ExpertPlan), _p],
     "svla_expert_status": [ctypes.POINTER(ExpertPlan), ctypes.POINTER(ctypes.c_int)],
+    "svla_expert_trace_offset": [ctypes.POINTER(ExpertDesc), _i, _i],
 }
 
-RESTYPES = {"svla_expert_workspace_size": ctypes.c_long}
+RESTYPES = {"svla_expert_workspace_size": ctypes.c_long,
+            "svla_expert_trace_offset": ctypes.c_long}
 
 _LIB = None
 

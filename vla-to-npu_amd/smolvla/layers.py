@@ -24,6 +24,7 @@ import math
 from dataclasses import dataclass
 from typing import Optional
 
+import numpy as np
 import torch
 
 from . import ops
@@ -33,8 +34,32 @@ BF16 = torch.bfloat16
 
 
 # ------------------------------------------------------------ weight prep ---
+def is_bf16_bits(a):
+    """A numpy array holding bfloat16 values as 2-byte words: the reference's
+    ``ml_dtypes.bfloat16`` arrays (``NP_DTYPE``, vla/text_encoder_bf16.py:55),
+    or raw ``uint16`` bit patterns of a caller without ml_dtypes."""
+    return a.dtype.itemsize == 2 and (a.dtype.name == "bfloat16" or a.dtype == np.uint16)
+
+
+def host_tensor(a):
+    """A torch tensor as is; a numpy array (how the reference builds ``params``
+    and its inputs, vla/text_encoder_bf16.py:599-609) as a CPU torch tensor:
+    floating arrays keep their values, bfloat16 words (:func:`is_bf16_bits`)
+    are reinterpreted bit for bit, integer ids stay integers."""
+    if torch.is_tensor(a):
+        return a
+    a = np.asarray(a)
+    if is_bf16_bits(a):
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(BF16)
+    if a.dtype.kind not in "fiub":
+        raise TypeError(f"unsupported array dtype {a.dtype}")
+    return torch.from_numpy(np.ascontiguousarray(a))
+
+
 def _dev(t, device):
-    return t.to(device=device, dtype=BF16).contiguous()
+    """A weight (torch tensor or numpy array) as a contiguous bf16 tensor on
+    ``device``."""
+    return host_tensor(t).to(device=device, dtype=BF16).contiguous()
 
 
 def _pack_cols(ws, device):
@@ -91,7 +116,7 @@ def prep_vit(p, device, wide=False):
     if p.get("bq") is not None:
         bqkv = torch.empty(3 * H, dtype=BF16, device=device)
         for i, k in enumerate(("bq", "bk", "bv")):
-            bqkv[i * H:(i + 1) * H].copy_(p[k])
+            bqkv[i * H:(i + 1) * H].copy_(_dev(p[k], device))
     opt = lambda k: _dev(p[k], device) if p.get(k) is not None else None  # noqa: E731
     P = dict(
         wqkv=_pack_cols([p["Wq"], p["Wk"], p["Wv"]], device), bqkv=bqkv,

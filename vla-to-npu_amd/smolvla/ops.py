@@ -94,19 +94,29 @@ class FusedExpert:
     def __init__(self, cfg, expert_layers, cross, io, rope, tbias, x_state, batch, dt,
                  team_xcd=-1):
         e = cfg.expert
-        self._keep = []                       # tensors the device table points at
+        # every tensor whose device address goes into the descriptor (and so
+        # into the uploaded phase table) is held here for the plan's lifetime
+        self._keep = []
+
+        def addr(t):
+            self._keep.append(t)
+            return _addr(t)
+
         layers = (_lib.ExpertLayer * cfg.expert_layers)()
+        ld_cross = 0                          # no cross layer: unused
         for i, P in enumerate(expert_layers):
             L = layers[i]
             L.cross = int(cfg.is_cross(i))
-            L.w_qkv = _addr(P["wq"] if L.cross else P["wqkv"])
-            L.w_o, L.w_gu, L.w_down = _addr(P["wo"]), _addr(P["wgu"]), _addr(P["wd"])
-            L.norm1, L.norm2 = _addr(P["n1"]), _addr(P["n2"])
+            L.w_qkv = addr(P["wq"] if L.cross else P["wqkv"])
+            L.w_o, L.w_gu, L.w_down = addr(P["wo"]), addr(P["wgu"]), addr(P["wd"])
+            L.norm1, L.norm2 = addr(P["n1"]), addr(P["n2"])
             if L.cross:
                 ck, cv = cross[i]
                 if ck.stride(0) != cv.stride(0):
                     raise ValueError("cross K and V need one leading dimension")
-                L.cross_k, L.cross_v = _addr(ck), _addr(cv)
+                if ld_cross and ck.stride(0) != ld_cross:
+                    raise ValueError("every cross layer's K/V needs the same leading dimension")
+                L.cross_k, L.cross_v = addr(ck), addr(cv)
                 ld_cross = ck.stride(0)
         d = _lib.ExpertDesc()
         d.batch, d.chunk, d.hidden = batch, cfg.chunk, e.hidden
@@ -115,12 +125,12 @@ class FusedExpert:
         d.num_steps, d.ld_cross = cfg.num_steps, ld_cross
         from .config import resolve_eps
         d.rms_eps, d.dt = resolve_eps(e.rms_eps), float(dt)
-        d.w_action_in, d.b_action_in = _addr(io["w_ain"]), _addr(io["b_ain"])
-        d.w_time_in_a, d.time_bias = _addr(io["w_tin_a"]), _addr(tbias)
-        d.w_time_out, d.b_time_out = _addr(io["w_tout"]), _addr(io["b_tout"])
-        d.norm_out, d.w_action_out = _addr(io["n_exp"]), _addr(io["w_aout"])
-        d.rope_cos, d.rope_sin = _addr(rope.cos), _addr(rope.sin)
-        d.x_in = d.x_out = _addr(x_state)
+        d.w_action_in, d.b_action_in = addr(io["w_ain"]), addr(io["b_ain"])
+        d.w_time_in_a, d.time_bias = addr(io["w_tin_a"]), addr(tbias)
+        d.w_time_out, d.b_time_out = addr(io["w_tout"]), addr(io["b_tout"])
+        d.norm_out, d.w_action_out = addr(io["n_exp"]), addr(io["w_aout"])
+        d.rope_cos, d.rope_sin = addr(rope.cos), addr(rope.sin)
+        d.x_in = d.x_out = addr(x_state)
         d.layers = layers
         lib = _lib.load()
         nbytes = lib.svla_expert_workspace_size(ctypes.byref(d))
@@ -128,10 +138,13 @@ class FusedExpert:
             raise ValueError("fused expert: configuration not supported")
         self.workspace = torch.empty(nbytes + 256, dtype=torch.uint8, device=x_state.device)
         base = (self.workspace.data_ptr() + 255) // 256 * 256
+        self._base = base - self.workspace.data_ptr()
         self.plan = _lib.ExpertPlan()
         _lib.call("svla_expert_prepare", ctypes.byref(d), ctypes.c_void_p(base), nbytes,
                   int(team_xcd), ctypes.byref(self.plan), _stream())
         self.desc, self.layers = d, layers
+        self.rows, self.hidden = batch * cfg.chunk, e.hidden
+        self._frag_idx = None
 
     def run(self):
         _lib.call("svla_expert_run", ctypes.byref(self.plan), _stream())
@@ -140,6 +153,26 @@ class FusedExpert:
         st = ctypes.c_int(-1)
         _lib.call("svla_expert_status", ctypes.byref(self.plan), ctypes.byref(st))
         return st.value
+
+    def trace(self, step, layer):
+        """The activation entering expert layer ``layer`` at Euler step
+        ``step`` of the last run (``layer == n_layers``: the last layer's
+        output), ``[batch * chunk, hidden]`` bf16, read back from the
+        workspace (``svla_expert_trace_offset``; a copy, in stream order)."""
+        off = _lib.load().svla_expert_trace_offset(ctypes.byref(self.desc), int(step), int(layer))
+        if off < 0:
+            raise ValueError(f"no traced activation for step {step}, layer {layer}")
+        M, H = self.rows, self.hidden
+        nbytes = ((H + 31) // 32) * 4096          # bytes of a fragment-major [64, H] buffer
+        start = self._base + off
+        frag = self.workspace[start:start + nbytes].view(BF16)
+        if self._frag_idx is None:
+            # element (m, k) of a fragment-major buffer (svla.h)
+            m = torch.arange(M, device=frag.device)[:, None]
+            k = torch.arange(H, device=frag.device)[None, :]
+            self._frag_idx = ((((k // 32) * 4 + m // 16) * 64 + m % 16 + 16 * ((k // 8) % 4)) * 8
+                              + k % 8)
+        return frag[self._frag_idx]
 
 
 def init(device=None):

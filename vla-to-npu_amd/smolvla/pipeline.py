@@ -269,13 +269,29 @@ class SmolVLAEngine:
         else:
             self._forward()
 
+    def check(self):
+        """Raise if the last chunk's fused expert gave up (its status word is
+        non-zero: a wait timed out, e.g. because other work held CUs the
+        persistent launch needed, or its XCD team did not form).  Such a
+        chunk's actions are NaN-filled by the kernel as well.  Synchronous."""
+        if self.fx is None:
+            return
+        st = self.fx.status()
+        if st != 0:
+            what = {1: "a phase wait timed out", 2: "the XCD team did not form"}.get(st, "?")
+            raise RuntimeError(f"fused action expert failed (status {st}: {what}); the "
+                               "chunk's actions are invalid")
+
     def run(self, images, lang_ids, state, noise):
         """images ``[B, cams, 3, H, W]`` bf16, lang_ids ``[B, 48]``, state
-        ``[B, 32]``, noise ``[B, 50, 32]`` fp32 -> actions ``[B, 50, 32]`` fp32."""
+        ``[B, 32]``, noise ``[B, 50, 32]`` fp32 -> actions ``[B, 50, 32]`` fp32.
+        Raises if the fused expert reports a failure (:meth:`check`)."""
         with torch.cuda.device(self.device):
             self.load_inputs(images, lang_ids, state, noise)
             self.step()
-            return self.x_t.view(self.B, self.cfg.chunk, self.cfg.action_dim).clone()
+            out = self.x_t.view(self.B, self.cfg.chunk, self.cfg.action_dim).clone()
+            self.check()
+            return out
 
     # intermediate views (tests)
     def prefix_view(self):

@@ -2,20 +2,42 @@
 
 from __future__ import annotations
 
+import collections
+
+import numpy as np
 import torch
+import xxhash
+
+from ..layers import host_tensor
 
 BF16 = torch.bfloat16
-_PREP_KEY = "__svla_prepared__"
+
+
+def _numpy_bf16(t):
+    """bf16 CPU tensor -> numpy: ``ml_dtypes.bfloat16`` (the reference's
+    ``NP_DTYPE``) when that package is importable, else float32 holding the
+    same (exactly representable) values."""
+    try:
+        import ml_dtypes
+    except ImportError:
+        return t.float().numpy()
+    return t.contiguous().view(torch.int16).numpy().view(ml_dtypes.bfloat16)
 
 
 def to_device(x):
-    """Accept a CPU/GPU tensor or a numpy array; return (bf16 GPU tensor,
-    function mapping a GPU result back to the caller's device)."""
-    if not torch.is_tensor(x):
-        x = torch.as_tensor(x)
+    """Accept a CPU/GPU tensor or a numpy array (fp32/fp16/fp64, or bfloat16
+    words as the reference's ``ml_dtypes`` arrays hold them); return (bf16 GPU
+    tensor, function mapping a GPU result back to the caller's kind: a GPU
+    tensor as is, a CPU tensor for a CPU tensor, a numpy array for a numpy
+    array -- the reference's callers use numpy methods on the result, e.g.
+    ``allo_out.astype(np.float32)``, vla/text_encoder_bf16.py:630)."""
+    was_numpy = not torch.is_tensor(x)
+    x = host_tensor(x) if was_numpy else x
     if x.is_cuda:
         return x.to(BF16), (lambda t: t)
     dev = torch.device("cuda")
+    if was_numpy:
+        return x.to(device=dev, dtype=BF16), (lambda t: _numpy_bf16(t.cpu()))
     return x.to(device=dev, dtype=BF16), (lambda t: t.cpu())
 
 
@@ -26,10 +48,43 @@ def as_batched(x):
     return x, False
 
 
+# Packed weights of recently used params dicts.  Kept here, not in the
+# caller's dict: an entry is reused only while the dict holds the very same
+# weight objects with unchanged contents (torch tensors: the version counter
+# every in-place update bumps; numpy arrays: a content hash), so an updated
+# weight is re-packed, never served stale.
+_PREPARED = collections.OrderedDict()
+_PREPARED_MAX = 64
+
+
+def _state(params):
+    vals, marks = [], []
+    for k in sorted(params, key=str):
+        v = params[k]
+        vals.append(v)
+        if torch.is_tensor(v):
+            marks.append((k, v._version))
+        elif isinstance(v, np.ndarray):
+            a = np.ascontiguousarray(v)
+            marks.append((k, xxhash.xxh3_64_intdigest(a.reshape(-1).view(np.uint8))))
+        else:
+            marks.append((k, repr(v)))
+    return vals, tuple(marks)
+
+
 def prepared(params, prep_fn):
-    """Pack reference-layout weights once per params dict (cached in it)."""
-    cache = params.get(_PREP_KEY)
-    if cache is None or cache[0] is not prep_fn:
-        cache = (prep_fn, prep_fn(params, torch.device("cuda")))
-        params[_PREP_KEY] = cache
-    return cache[1]
+    """Pack reference-layout weights (torch tensors or the reference's numpy
+    arrays, ``[in, out]``) once per params dict and weight state."""
+    key = (id(params), prep_fn)
+    vals, marks = _state(params)
+    hit = _PREPARED.get(key)
+    if hit is not None and hit[1] == marks and len(hit[0]) == len(vals) and all(
+            a is b for a, b in zip(hit[0], vals)):
+        _PREPARED.move_to_end(key)
+        return hit[2]
+    out = prep_fn(params, torch.device("cuda"))
+    _PREPARED[key] = (vals, marks, out)     # holds the weight objects: ids stay unique
+    _PREPARED.move_to_end(key)
+    while len(_PREPARED) > _PREPARED_MAX:
+        _PREPARED.popitem(last=False)
+    return out

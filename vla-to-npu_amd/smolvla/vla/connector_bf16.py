@@ -9,8 +9,8 @@ The shuffle is folded into the GEMM's A-operand addressing.  ``x`` may be
 
 from __future__ import annotations
 
-from .. import ops
-from ._common import to_device
+from .. import layers, ops
+from ._common import prepared, to_device
 
 SEQ = 1024
 EMBD = 768
@@ -20,15 +20,15 @@ NEW_EMBD = 12288
 TEXT = 960
 
 
+def _prep_connector(p, device):
+    return ops.pack_weight(layers._dev(p["W"], device))
+
+
 def connector_block(x_np, params, scale=SCALE_FACTOR):
     x, back = to_device(x_np)
     squeeze = x.dim() == 2
     x3 = x.unsqueeze(0) if squeeze else x
-    key = "__svla_conn_w__"
-    w = params.get(key)
-    if w is None:
-        w = ops.pack_weight(params["W"].to(device=x.device, dtype=x.dtype).contiguous())
-        params[key] = w
+    w = prepared(params, _prep_connector)
     out = ops.connector(x3.contiguous(), w, scale)
     n = x3.shape[0]
     return back(out if squeeze else out.view(n, -1, out.shape[1]))

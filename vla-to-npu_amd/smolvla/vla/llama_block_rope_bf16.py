@@ -33,7 +33,7 @@ def llama_block_rope(x_np, params, cfg: DecoderConfig = DEFAULT_CFG):
 
 
 def _prep_q_only(p, device):
-    d = lambda t: t.to(device=device, dtype=torch.bfloat16).contiguous()  # noqa: E731
+    d = lambda t: layers._dev(t, device)  # noqa: E731
     return dict(
         wq=ops.pack_weight(d(p["Wq"])), wo=ops.pack_weight(d(p["Wo"])),
         wgu=ops.pack_gate_up(d(p["W_gate"]), d(p["W_up"])), wd=ops.pack_weight(d(p["W_down"])),

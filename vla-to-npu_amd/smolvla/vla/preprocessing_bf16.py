@@ -11,6 +11,7 @@ with the optional conv ``bias`` and learned position embedding ``pos_emb``
 from __future__ import annotations
 
 from .. import ops
+from ..layers import _dev
 from ._common import to_device
 
 CHANNELS = 3
@@ -24,13 +25,13 @@ def preprocessing_block(x_np, params):
     img, back = to_device(x_np)
     squeeze = img.dim() == 3
     img4 = img.unsqueeze(0) if squeeze else img
-    kern = params["kernel"]
+    kern = _dev(params["kernel"], img.device)
     E, C, P, _ = kern.shape
-    w = kern.to(device=img.device, dtype=img.dtype).reshape(E, C * P * P).contiguous()
+    w = kern.reshape(E, C * P * P).contiguous()
     bias = params.get("bias")
     pos = params.get("pos_emb")
-    bias = bias.to(device=img.device, dtype=img.dtype).contiguous() if bias is not None else None
-    pos = pos.to(device=img.device, dtype=img.dtype).contiguous() if pos is not None else None
+    bias = _dev(bias, img.device) if bias is not None else None
+    pos = _dev(pos, img.device) if pos is not None else None
     out = ops.patch_embed(img4.contiguous(), w, bias, pos, P)
     n = img4.shape[0]
     return back(out if squeeze else out.view(n, -1, E))

@@ -19,6 +19,7 @@ import torch
 
 from .. import ops
 from ..config import DecoderConfig, resolve_eps
+from ..layers import _dev, host_tensor
 from ..pipeline import SmolVLAEngine
 from ._common import to_device
 from .action_expert_bf16 import action_expert_cross_forward, action_expert_self_forward
@@ -31,8 +32,8 @@ MAX_STATE_DIM = 32
 
 
 def create_text_emb(lang_tokens, table):
-    ids = torch.as_tensor(lang_tokens).to("cuda").reshape(-1)
-    t = table.to(device="cuda", dtype=torch.bfloat16).contiguous()
+    ids = host_tensor(lang_tokens).to("cuda").reshape(-1)
+    t = _dev(table, "cuda")
     out = torch.empty(ids.numel(), t.shape[1], dtype=torch.bfloat16, device="cuda")
     return ops.embed(ids, t, math.sqrt(t.shape[1]), out)
 
@@ -40,7 +41,7 @@ def create_text_emb(lang_tokens, table):
 def create_state_emb(state_input, weights):
     s, back = to_device(state_input)
     s2 = s.reshape(-1, s.shape[-1]).contiguous()
-    w = ops.pack_weight(weights.to(device="cuda", dtype=torch.bfloat16).contiguous())
+    w = ops.pack_weight(_dev(weights, "cuda"))
     return back(ops.linear(s2, w))
 
 
@@ -66,10 +67,9 @@ def joint_transformer(num_layers, vlm_input, action, vlm_params, exp_self_params
 def postprocessing(out, out_params, eps=1e-5):
     x, back = to_device(out)
     x2 = x.reshape(-1, x.shape[-1]).contiguous()
-    w = out_params["W_exp_norm"].to(device="cuda", dtype=torch.bfloat16).contiguous()
+    w = _dev(out_params["W_exp_norm"], "cuda")
     h = ops.rmsnorm(x2, w, resolve_eps(eps))
-    wo = ops.pack_weight(out_params["W_action_out"].to(device="cuda",
-                                                       dtype=torch.bfloat16).contiguous())
+    wo = ops.pack_weight(_dev(out_params["W_action_out"], "cuda"))
     return back(ops.linear(h, wo))
 
 
