@@ -227,6 +227,17 @@ int svla_linear_rope_bf16(const void* a, int lda, const void* w, int ldw, void* 
                           const float* sin_t, const void* norm_w, float norm_eps,
                           svla_stream_t stream);
 
+/* svla_linear_rope_bf16 that also writes, for every rotated column, the bf16
+ * remainder c_lo = o - bf16(o) of the fp32 RoPE output o (c_lo: same ldc and
+ * row layout as c; columns past rope_cols are not written; NULL: none).  The
+ * reference module keeps Q and K in fp32 after RoPE and scores them in fp32
+ * (vla/text_encoder_bf16.py:92-104, 117-122); bf16 hi + lo carries o to about
+ * 16 bits for svla_attention_lo_bf16. */
+int svla_linear_rope_lo_bf16(const void* a, int lda, const void* w, int ldw, void* c,
+                             void* c_lo, int ldc, int m, int n, int k, int rope_cols, int seq_len,
+                             const float* cos_t, const float* sin_t, const void* norm_w,
+                             float norm_eps, svla_stream_t stream);
+
 /* Gated MLP up-projection: out[M, inter] = bf16(silu(gate)) * bf16(up) (bf16),
  * gate/up from one GEMM over the weight interleaved by svla_pack_gate_up_bf16
  * (optionally on RMS-normalised A).  Replaces rmsnorm + gemm_ffn_up x2 +
@@ -391,6 +402,19 @@ int svla_attention_bf16(const void* q, int ldq, long q_bs, const void* k, int ld
                         const void* v, int ldv, long v_bs, void* o, int ldo, long o_bs,
                         int batch, int sq, int sk, int hq, int hkv, int head_dim, float scale,
                         int mask_kind, int prefix_len, svla_stream_t stream);
+
+/* svla_attention_bf16 with fp32-accurate scores for RoPE'd Q and K: q_lo /
+ * k_lo (nullable; k_lo only with q_lo) are the bf16 remainders written by
+ * svla_linear_rope_lo_bf16, with the strides of q / k; the scores are then
+ * K . Q^T for Q = q + q_lo, K = k + k_lo (the k_lo . q_lo term, below 2^-16
+ * relative, is dropped), as the reference module scores its fp32 post-RoPE
+ * Q and K (vla/text_encoder_bf16.py:117-122; vla/action_expert_bf16.py:
+ * 119-125, 194-199: Q only in cross layers, whose K is a plain projection). */
+int svla_attention_lo_bf16(const void* q, const void* q_lo, int ldq, long q_bs, const void* k,
+                           const void* k_lo, int ldk, long k_bs, const void* v, int ldv,
+                           long v_bs, void* o, int ldo, long o_bs, int batch, int sq, int sk,
+                           int hq, int hkv, int head_dim, float scale, int mask_kind,
+                           int prefix_len, svla_stream_t stream);
 
 /* -------------------------------------------------- per-kernel harness --
  * Standalone kernels matching the reference's per-kernel test harness. */

@@ -104,7 +104,8 @@ def test_full_config_fused_expert_per_layer(full1):
     reference checks each expert layer on its own
     (vla/action_expert_bf16.py:848-906).  Steps 0 and 9; plus the step-0
     expert input against the oracle's action/time embedding, and the 16
-    layers chained from the oracle's own step-0 input."""
+    layers chained from the oracle's own step-0 input.  The layer-by-layer
+    kernels (the batch-32 path) run on the same inputs to the same bound."""
     cfg, P, inputs, _ = full1
     dev = [t.cuda() for t in inputs]
     eng = _engine(cfg, P, 1)
@@ -113,7 +114,8 @@ def test_full_config_fused_expert_per_layer(full1):
     e, L, Lc = cfg.expert, cfg.chunk, cfg.prefix_len
     ckv = {i: (ck.cpu().reshape(1, Lc, -1), cv.cpu().reshape(1, Lc, -1))
            for i, (ck, cv) in eng.cross.items()}
-    worst = 0.0
+    from smolvla import layers
+    worst = worst_l = 0.0
     with torch.inference_mode():
         for step in (0, cfg.num_steps - 1):
             for li in range(cfg.expert_layers):
@@ -127,6 +129,17 @@ def test_full_config_fused_expert_per_layer(full1):
                 err = _rel(got, want)
                 worst = max(worst, err)
                 assert err <= LAYER_RTOL, f"step {step} layer {li}: {err:.3e}"
+                # the layer-by-layer kernels (the batch-32 path) on the same
+                # real expert activations
+                xl = x.reshape(L, e.hidden).cuda().clone()
+                if cfg.is_cross(li):
+                    ck, cv = eng.cross[li]
+                    layers.cross_layer(xl, ck, cv, eng.expert[li], e, 1, L, Lc, eng.rope_expert)
+                else:
+                    layers.decoder_layer(xl, eng.expert[li], e, 1, L, eng.rope_expert, "causal")
+                err_l = _rel(xl.cpu().view(1, L, e.hidden), want)
+                worst_l = max(worst_l, err_l)
+                assert err_l <= LAYER_RTOL, f"layered, step {step} layer {li}: {err_l:.3e}"
         # step 0's expert input: action_in / time MLP of the noise at t = 1
         h0 = ref.expert_input(inputs[3].float(), 1.0, P, cfg)
         e_in = _rel(eng.fx.trace(0, 0).cpu().view(1, L, e.hidden), h0)
@@ -139,7 +152,8 @@ def test_full_config_fused_expert_per_layer(full1):
                  else ref.expert_self_block(h, lp, e))
             e_ch = _rel(eng.fx.trace(0, li + 1).cpu().view(1, L, e.hidden), h)
             assert e_ch <= CHAIN_RTOL, f"chain layer {li}: {e_ch:.3e}"
-    print(f"fused expert per layer: worst {worst:.3e}, input {e_in:.3e}, chain end {e_ch:.3e}")
+    print(f"fused expert per layer: worst {worst:.3e} (layer-by-layer kernels {worst_l:.3e}), "
+          f"input {e_in:.3e}, chain end {e_ch:.3e}")
 
 
 def test_run_raises_on_expert_status():

@@ -517,6 +517,38 @@ def test_linear_rope_qkv(ops, M, L, hid):
     assert_close_bf16(got[:, 1280:], v)
 
 
+@pytest.mark.parametrize("M,L,hid", [(241, 241, 960), (100, 50, 720), (7712, 241, 960)])
+def test_linear_rope_remainder(ops, M, L, hid):
+    """The RoPE epilogue's optional remainder output: hi is bit-identical to the
+    plain call, lo = o - bf16(o) of the fp32 rotation, so hi + lo follows the
+    fp32 RoPE of the bf16 projection (the reference's Q and K,
+    vla/text_encoder_bf16.py:92-104) to ~2^-16 wherever the projection rounds
+    like torch's (rarely 1 bf16 ulp apart: a few elements); V columns of lo
+    are left untouched."""
+    g = gen(M + 7 * hid)
+    theta = 100000.0
+    x = randn(g, M, hid)
+    w = randn(g, hid, 1600, std=0.02)
+    wp = ops.pack_weight(w.cuda())
+    cos_t, sin_t = ops.rope_table(L, 64, theta)
+    plain = ops.linear_rope(x.cuda(), wp, 1280, L, cos_t, sin_t).cpu()
+    lo = torch.full((M, 1600), 7.0, dtype=BF16, device="cuda")
+    hi = ops.linear_rope(x.cuda(), wp, 1280, L, cos_t, sin_t, out_lo=lo).cpu()
+    lo = lo.cpu()
+    assert torch.equal(hi, plain)
+    assert (lo[:, 1280:] == 7.0).all()
+    B = M // L
+    proj = ref.linear(x, w)                                   # bf16, as the kernel rounds it
+    q = ref.apply_rope(proj[:, :960].reshape(B, L, 15, 64), theta).reshape(M, 960)
+    k = ref.apply_rope(proj[:, 960:1280].reshape(B, L, 5, 64), theta).reshape(M, 320)
+    want = torch.cat([q, k], dim=1)                           # fp32
+    got = hi[:, :1280].float() + lo[:, :1280].float()
+    err = (got - want).abs() / want.abs().clamp_min(1e-3)
+    assert (lo[:, :1280].float().abs() <= hi[:, :1280].float().abs() * 2 ** -8 + 1e-30).all()
+    assert (err <= 2 ** -15).float().mean().item() >= 0.99, err.median().item()
+    assert (got - want).abs().max().item() <= 2e-2
+
+
 @pytest.mark.parametrize("M,K,inter", [(50, 720, 2048), (241, 960, 2560), (1024, 960, 2560),
                                        (5, 64, 64), (7712, 960, 2560), (3000, 720, 2048)])
 def test_linear_silu_mul(ops, M, K, inter):
@@ -602,6 +634,37 @@ def test_attention(ops, B, Sq, Sk, hq, hkv, mask, prefix):
                              v.view(B, Sk, hkv, 64), m)
     assert rel_err(out, want) <= 1e-2
     torch.testing.assert_close(out.cpu().float(), want.float(), atol=2e-2, rtol=2e-2)
+
+
+@pytest.mark.parametrize("B,S,Sk,mask,with_k", [(2, 241, 241, "prefix_lm", True),
+                                                (3, 50, 50, "causal", True),
+                                                (2, 50, 241, "none", False),
+                                                (1, 128, 128, "causal", True)])
+def test_attention_fp32_qk_remainders(ops, B, S, Sk, mask, with_k):
+    """Scores on fp32 Q (and K) carried as bf16 hi + lo (svla_attention_lo_bf16)
+    against the oracle's attention on the fp32 values, the reference module's
+    own precision (vla/text_encoder_bf16.py:117-122): several times closer
+    than the plain bf16 call, and within 1e-2."""
+    g = gen(B * 77 + S + Sk)
+    qf = torch.randn(B, S, 960, generator=g) * 2.0
+    kf = torch.randn(B, Sk, 320, generator=g) * 2.0
+    v = randn(g, B, Sk, 320)
+    split = lambda t: (t.to(BF16), (t - t.to(BF16).float()).to(BF16))  # noqa: E731
+    qh, ql = split(qf)
+    kh, kl = split(kf)
+    if not with_k:                                # cross layers: K is a plain bf16 projection
+        kf, kl = kh.float(), None
+    prefix = 240 if mask == "prefix_lm" else 0
+    m = ref.make_mask(mask, S, Sk, prefix)
+    want = ref.gqa_attention(qf.view(B, S, 15, 64), kf.view(B, Sk, 5, 64), v.view(B, Sk, 5, 64), m)
+    out = torch.empty(B, S, 960, dtype=BF16, device="cuda")
+    ops.attention(qh.cuda(), kh.cuda(), v.cuda(), out, 15, 5, mask, prefix, q_lo=ql.cuda(),
+                  k_lo=kl.cuda() if kl is not None else None)
+    plain = torch.empty_like(out)
+    ops.attention(qh.cuda(), kh.cuda(), v.cuda(), plain, 15, 5, mask, prefix)
+    e_lo, e_plain = rel_err(out, want), rel_err(plain, want)
+    print(f"fp32-QK attention: with remainders {e_lo:.3e}, plain bf16 {e_plain:.3e}")
+    assert e_lo <= 1e-2 and e_lo <= e_plain
 
 
 def test_attention_views_into_fused_qkv(ops):

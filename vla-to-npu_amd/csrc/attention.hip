@@ -30,6 +30,10 @@ constexpr int kAttnCUs = 256;  // MI355X compute units
 struct AttnArgs {
   const bf16* q; long ldq, q_bs;
   const bf16* k; long ldk, k_bs;
+  // optional bf16 remainders of fp32 Q and K (same layout and strides as q,
+  // k): the scores are then K . Q^T with Q = q + q_lo, K = k + k_lo
+  const bf16* q_lo;
+  const bf16* k_lo;
   const bf16* v; long ldv, v_bs;
   bf16* o; long ldo, o_bs;
   int sq, sk, hq, hkv;
@@ -75,6 +79,14 @@ __device__ __forceinline__ float max_xor32(float x) {
   const u32x2_t r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return smax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+__device__ __forceinline__ float sum_xor16(float x) {
+  const u32x2_t r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const u32x2_t r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 typedef __attribute__((address_space(3))) v4i16* lds_v4i16_ptr;
 
 // V^T operand of O^T += V^T . P^T via the LDS transpose read: within each
@@ -102,11 +114,24 @@ __device__ __forceinline__ v4i16 v_tr_read(const bf16* sv, int kbase, int dbase,
 // {4g..4g+3} u {16+4g..16+4g+3} in k-slots 8g..8g+7, g = lane / 16); the V^T
 // operand is read with the same key order.
 // FULL: no mask and sk % 64 == 0, so no per-score checks at all.
-template <bool FULL, int QT>
+// LO: 0 plain bf16 Q and K; 1 Q = q + q_lo (the fp32 RoPE output as two bf16
+// parts: S^T gains K . q_lo^T); 2 also K = k + k_lo (K_lo streams through a
+// third ring beside K and V; S^T gains k_lo . q^T).  The reference scores
+// the fp32 post-RoPE Q and K (vla/text_encoder_bf16.py:92-104, 117-122).
+// With LO > 0 the softmax is also the reference's exactly, in two passes over
+// the key blocks: the first takes each query's maximum m and fp32 sum
+// l = sum exp(s - m), the second recomputes the scores and rounds
+// p = bf16(exp(s - m) * (1 / l)) -- the normalised fp32 probability, as torch's
+// softmax(...).to(bf16) -- before P.V (the one-pass form below rounds the
+// unnormalised exponentials and divides by the sum of the rounded values at
+// the end).  These RoPE'd layers have at most a few hundred keys.
+template <bool FULL, int QT, int LO>
 __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
   constexpr int QW = ::QW<QT>, BQ = ::BQ<QT>;
+  constexpr int KLO = LO == 2 ? BKEY * D : 64;  // K remainder stages (LO == 2 only)
   __shared__ __attribute__((aligned(1024))) bf16 sK0[BKEY * D], sK1[BKEY * D], sK2[BKEY * D];
   __shared__ __attribute__((aligned(1024))) bf16 sV0[BKEY * D], sV1[BKEY * D], sV2[BKEY * D];
+  __shared__ __attribute__((aligned(1024))) bf16 sL0[KLO], sL1[KLO], sL2[KLO];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int h = blockIdx.y, b = blockIdx.z;
@@ -117,6 +142,8 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
 
   const bf16* qb = p.q + b * p.q_bs + h * D;
   const bf16* kb = p.k + b * p.k_bs + kvh * D;
+  const bf16* qlb = LO >= 1 ? p.q_lo + b * p.q_bs + h * D : nullptr;
+  const bf16* klb = LO == 2 ? p.k_lo + b * p.k_bs + kvh * D : nullptr;
   const bf16* vb = p.v + b * p.v_bs + kvh * D;
 
   // last key any row of this workgroup may see
@@ -145,6 +172,7 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
     constexpr int S = decltype(SI)::value;
     bf16* sk = S == 0 ? sK0 : S == 1 ? sK1 : sK2;
     bf16* sv = S == 0 ? sV0 : S == 1 ? sV1 : sV2;
+    bf16* sl = S == 0 ? sL0 : S == 1 ? sL1 : sL2;
     blk = min(blk, nb - 1);  // past the end: reload the last block (never read)
     const int k0 = blk * BKEY;
 #pragma unroll
@@ -153,15 +181,20 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
       // (never in FULL) needs per-lane clamping of rows past sk
       const bf16* gk = kb + (long)k0 * p.ldk + koff[j];
       const bf16* gv = vb + (long)k0 * p.ldv + voff[j];
+      long adj = 0;
       if constexpr (!FULL) {
         const int key = (wave * 2 + j) * 8 + (lane >> 3);
         const int rows_left = p.sk - 1 - k0;
-        const long adj = key > rows_left ? (long)(rows_left - key) : 0;
+        adj = key > rows_left ? (long)(rows_left - key) : 0;
         gk += adj * p.ldk;
         gv += adj * p.ldv;
       }
       __builtin_amdgcn_global_load_lds((void*)gk, (lds_ptr_t)(sk + (wave * 2 + j) * 512), 16, 0, 0);
       __builtin_amdgcn_global_load_lds((void*)gv, (lds_ptr_t)(sv + (wave * 2 + j) * 512), 16, 0, 0);
+      if constexpr (LO == 2) {
+        const bf16* gl = klb + ((long)k0 + adj) * p.ldk + koff[j];
+        __builtin_amdgcn_global_load_lds((void*)gl, (lds_ptr_t)(sl + (wave * 2 + j) * 512), 16, 0, 0);
+      }
     }
   };
 
@@ -169,11 +202,16 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
   // Rows past sq are clamped (their outputs are never stored); loading
   // without a branch keeps the loads in flight across the DMA prologue.
   bf16x8 qf[QT][2];
+  bf16x8 qlf[LO >= 1 ? QT : 1][2];  // Q remainders (LO >= 1)
 #pragma unroll
   for (int qt = 0; qt < QT; ++qt) {
     const int qi = min(qw + qt * 16 + col, p.sq - 1);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) qf[qt][ks] = ld8(qb + (long)qi * p.ldq + ks * 32 + grp * 8);
+    if constexpr (LO >= 1) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) qlf[qt][ks] = ld8(qlb + (long)qi * p.ldq + ks * 32 + grp * 8);
+    }
   }
 
   // o[qt][0..3]: O^T tiles (head dims 16 t .. 16 t + 15); o[qt][4]: the
@@ -213,21 +251,30 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
     constexpr int S = decltype(SI)::value;
     const bf16* sk = S == 0 ? sK0 : S == 1 ? sK1 : sK2;
     const bf16* sv = S == 0 ? sV0 : S == 1 ? sV1 : sV2;
+    const bf16* sl = S == 0 ? sL0 : S == 1 ? sL1 : sL2;
     const int k0 = blk * BKEY;
     // S^T: 4 key subtiles x 2 query tiles, K fragments shared by both
     f32x4 sacc[4][QT];
 #pragma unroll
     for (int ts = 0; ts < 4; ++ts) {
-      bf16x8 kf[2];
+      bf16x8 kf[2], klf[LO == 2 ? 2 : 1];
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int ks = 0; ks < 2; ++ks) {
         kf[ks] = *reinterpret_cast<const bf16x8*>(&sk[kv_off(ts * 16 + col, ks * 32 + grp * 8)]);
+        if constexpr (LO == 2)
+          klf[ks] = *reinterpret_cast<const bf16x8*>(&sl[kv_off(ts * 16 + col, ks * 32 + grp * 8)]);
+      }
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
         f32x4 a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int ks = 0; ks < 2; ++ks) {
+          if constexpr (LO == 2)
+            a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klf[ks], qf[qt][ks], a, 0, 0, 0);
+          if constexpr (LO >= 1)
+            a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qlf[qt][ks], a, 0, 0, 0);
           a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[qt][ks], a, 0, 0, 0);
+        }
         sacc[ts][qt] = a;
       }
     }
@@ -299,13 +346,122 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
     }
   };
 
-  // Before each barrier: s_waitcnt vmcnt(4) lgkmcnt(0).  vmcnt: a stage is 4
-  // DMA instructions per wave and the next stage stays in flight.
+  // ---- exact two-pass softmax (LO > 0) ----
+  // scores of one block for every query tile, masked
+  auto scores = [&](const bf16* sk, const bf16* sl, int k0, f32x4 (&sacc)[4][QT]) {
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts) {
+      bf16x8 kf[2], klf[LO == 2 ? 2 : 1];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        kf[ks] = *reinterpret_cast<const bf16x8*>(&sk[kv_off(ts * 16 + col, ks * 32 + grp * 8)]);
+        if constexpr (LO == 2)
+          klf[ks] = *reinterpret_cast<const bf16x8*>(&sl[kv_off(ts * 16 + col, ks * 32 + grp * 8)]);
+      }
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          if constexpr (LO == 2)
+            a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(klf[ks], qf[qt][ks], a, 0, 0, 0);
+          if constexpr (LO >= 1)
+            a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qlf[qt][ks], a, 0, 0, 0);
+          a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks], qf[qt][ks], a, 0, 0, 0);
+        }
+        sacc[ts][qt] = a;
+      }
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      if (k0 + BKEY > kmin[qt]) {
+#pragma unroll
+        for (int ts = 0; ts < 4; ++ts)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kj = k0 + ts * 16 + grp * 4 + i;
+            sacc[ts][qt][i] = kj < klim[qt] ? sacc[ts][qt][i] : -INFINITY;
+          }
+      }
+    }
+  };
+  // pass 1: running maximum and the fp32 sum of exp(s - m), rescaled as the
+  // maximum moves (m_run, l_run per query tile)
+  float l_run[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; ++qt) l_run[qt] = 0.f;
+  auto stats = [&](auto SI, int blk) {
+    constexpr int S = decltype(SI)::value;
+    const bf16* sk = S == 0 ? sK0 : S == 1 ? sK1 : sK2;
+    const bf16* sl = S == 0 ? sL0 : S == 1 ? sL1 : sL2;
+    f32x4 sacc[4][QT];
+    scores(sk, sl, blk * BKEY, sacc);
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      float mx = sacc[0][qt][0];
+#pragma unroll
+      for (int ts = 0; ts < 4; ++ts)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = smax(mx, sacc[ts][qt][i]);
+      mx = max_xor32(max_xor16(mx));
+      const float m_new = smax(m_run[qt], mx);
+      const float off = -((m_new == -INFINITY ? 0.f : m_new) * c);
+      const float alpha = m_run[qt] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(__builtin_fmaf(m_run[qt], c, off));
+      float sum = 0.f;
+#pragma unroll
+      for (int ts = 0; ts < 4; ++ts)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sum += __builtin_amdgcn_exp2f(__builtin_fmaf(sacc[ts][qt][i], c, off));
+      sum = sum_xor32(sum_xor16(sum));
+      l_run[qt] = __builtin_fmaf(l_run[qt], alpha, sum);
+      m_run[qt] = m_new;
+      m_off[qt] = off;
+    }
+  };
+  // pass 2: p = bf16(exp(s - m) * (1 / l)), O^T += V^T . P^T
+  float rl[QT];
+  auto accum = [&](auto SI, int blk) {
+    constexpr int S = decltype(SI)::value;
+    const bf16* sk = S == 0 ? sK0 : S == 1 ? sK1 : sK2;
+    const bf16* sv = S == 0 ? sV0 : S == 1 ? sV1 : sV2;
+    const bf16* sl = S == 0 ? sL0 : S == 1 ? sL1 : sL2;
+    f32x4 sacc[4][QT];
+    scores(sk, sl, blk * BKEY, sacc);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf16x8 vf[4];
+#pragma unroll
+      for (int td = 0; td < 4; ++td) {
+        const v4i16 lo = v_tr_read(sv, kk * 32 + 4 * grp, td * 16, col);
+        const v4i16 hi = v_tr_read(sv, kk * 32 + 16 + 4 * grp, td * 16, col);
+        const v4i16 w8[2] = {lo, hi};
+        vf[td] = *reinterpret_cast<const bf16x8*>(w8);
+      }
+#pragma unroll
+      for (int qt = 0; qt < QT; ++qt) {
+        bf16x8 pf;
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            pf[h * 4 + i] = f2bf(__builtin_amdgcn_exp2f(
+                                     __builtin_fmaf(sacc[2 * kk + h][qt][i], c, m_off[qt])) *
+                                 rl[qt]);
+#pragma unroll
+        for (int td = 0; td < 4; ++td)
+          o[qt][td] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[td], pf, o[qt][td], 0, 0, 0);
+      }
+    }
+  };
+
+  // Before each barrier: s_waitcnt vmcnt(4) lgkmcnt(0) (vmcnt(6) with the K
+  // remainders).  vmcnt: a stage is 4 (6) DMA instructions per wave and the
+  // next stage stays in flight.
   // lgkmcnt(0): this wave's LDS reads of the stage computed before the
   // barrier have completed, since the DMA issued right after the barrier
   // refills that stage (the compiler would otherwise wait only at the reads'
   // first use, after the refill's issue).  gfx9 encoding, expcnt unconstrained.
-  constexpr int kWaitOne = 0x070 | 4;
+  constexpr int kWaitOne = 0x070 | (LO == 2 ? 6 : 4);
   auto sync_step = [&]() __attribute__((always_inline)) {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(kWaitOne);
@@ -318,25 +474,39 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
   // Q is needed by every block: wait for it here, before the DMA prologue,
   // so the compiler has no pending load to drain at the loop entry
   __builtin_amdgcn_s_waitcnt(0xF70);
-  issue(I0{}, 0);
-  issue(I1{}, 1);
   // masked / ragged kernel (short key ranges: the expert's 50 or 241 keys):
   // after the last block, leave at once (nb is uniform across the
   // workgroup), with no further refills of never-read blocks and no further
   // barrier rounds.  (The same exits in the FULL kernel measured 6-7% slower
   // on the ViT's 16-block loop, so that loop keeps its original form.)
-  for (int blk = 0; blk < nb; blk += 3) {
-    sync_step();
-    issue(I2{}, blk + 2);
-    compute(I0{}, blk);
-    if (!FULL && blk + 1 >= nb) break;
-    sync_step();
-    issue(I0{}, blk + 3);
-    if (blk + 1 < nb) compute(I1{}, blk + 1);
-    if (!FULL && blk + 2 >= nb) break;
-    sync_step();
-    issue(I1{}, blk + 4);
-    if (blk + 2 < nb) compute(I2{}, blk + 2);
+  auto ring = [&](auto&& comp) __attribute__((always_inline)) {
+    issue(I0{}, 0);
+    issue(I1{}, 1);
+    for (int blk = 0; blk < nb; blk += 3) {
+      sync_step();
+      issue(I2{}, blk + 2);
+      comp(I0{}, blk);
+      if (!FULL && blk + 1 >= nb) break;
+      sync_step();
+      issue(I0{}, blk + 3);
+      if (blk + 1 < nb) comp(I1{}, blk + 1);
+      if (!FULL && blk + 2 >= nb) break;
+      sync_step();
+      issue(I1{}, blk + 4);
+      if (blk + 2 < nb) comp(I2{}, blk + 2);
+    }
+  };
+  if constexpr (LO > 0) {
+    ring(stats);
+    // every DMA landed and every wave's reads of the ring done before the
+    // second pass refills it from block 0
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) rl[qt] = 1.0f / l_run[qt];
+    ring(accum);
+  } else {
+    ring(compute);
   }
   // drain the trailing (never read) DMA before the workgroup exits
   __builtin_amdgcn_s_waitcnt(0);
@@ -346,7 +516,8 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
     const int qi = qw + qt * 16 + col;
     if (qi >= p.sq) continue;
     const float l = o[qt][4][0];
-    const float inv = l > 0.f ? 1.0f / l : 0.f;
+    // (the exact two-pass form already normalised its probabilities)
+    const float inv = LO > 0 ? 1.0f : l > 0.f ? 1.0f / l : 0.f;
     bf16* orow = p.o + b * p.o_bs + (long)qi * p.ldo + h * D;
 #pragma unroll
     for (int td = 0; td < 4; ++td) {
@@ -360,11 +531,12 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
 
 }  // namespace
 
-extern "C" int svla_attention_bf16(const void* q, int ldq, long q_bs, const void* k, int ldk,
-                                   long k_bs, const void* v, int ldv, long v_bs, void* o, int ldo,
-                                   long o_bs, int batch, int sq, int sk, int hq, int hkv,
-                                   int head_dim, float scale, int mask_kind, int prefix_len,
-                                   svla_stream_t stream) {
+extern "C" int svla_attention_lo_bf16(const void* q, const void* q_lo, int ldq, long q_bs,
+                                      const void* k, const void* k_lo, int ldk, long k_bs,
+                                      const void* v, int ldv, long v_bs, void* o, int ldo,
+                                      long o_bs, int batch, int sq, int sk, int hq, int hkv,
+                                      int head_dim, float scale, int mask_kind, int prefix_len,
+                                      svla_stream_t stream) {
   if (head_dim != D || hq <= 0 || hkv <= 0 || hq % hkv || sq < 0 || sk <= 0 || batch < 0)
     return SVLA_EINVAL;
   if (mask_kind < SVLA_MASK_NONE || mask_kind > SVLA_MASK_PREFIX_LM) return SVLA_EINVAL;
@@ -373,16 +545,21 @@ extern "C" int svla_attention_bf16(const void* q, int ldq, long q_bs, const void
   if (ldq < hq * D || ldk < hkv * D || ldv < hkv * D || ldo < hq * D) return SVLA_EINVAL;
   if (!svla_aligned16(q) || !svla_aligned16(k) || !svla_aligned16(v) || ((uintptr_t)o & 7))
     return SVLA_EINVAL;
+  if ((q_lo && !svla_aligned16(q_lo)) || (k_lo && !svla_aligned16(k_lo)) || (k_lo && !q_lo))
+    return SVLA_EINVAL;
   if (sq == 0 || batch == 0) return SVLA_OK;
   AttnArgs p;
   p.q = static_cast<const bf16*>(q); p.ldq = ldq; p.q_bs = q_bs;
   p.k = static_cast<const bf16*>(k); p.ldk = ldk; p.k_bs = k_bs;
+  p.q_lo = static_cast<const bf16*>(q_lo);
+  p.k_lo = static_cast<const bf16*>(k_lo);
   p.v = static_cast<const bf16*>(v); p.ldv = ldv; p.v_bs = v_bs;
   p.o = static_cast<bf16*>(o); p.ldo = ldo; p.o_bs = o_bs;
   p.sq = sq; p.sk = sk; p.hq = hq; p.hkv = hkv;
   p.scale_log2 = scale * 1.4426950408889634f;
   p.mask_kind = mask_kind;
   p.prefix_len = prefix_len;
+  const int lo = k_lo ? 2 : q_lo ? 1 : 0;
   // 16 query rows per wave (64 per workgroup) for short query ranges and for
   // grids that would leave the CUs with about one 128-row workgroup each;
   // 32 rows per wave (K / V LDS reads shared by two query tiles) otherwise,
@@ -390,24 +567,39 @@ extern "C" int svla_attention_bf16(const void* q, int ldq, long q_bs, const void
   // two waves per SIMD) for unmasked grids of at least two 256-row
   // workgroups per CU, measured on MI355X: the batch-32 ViT attention (96
   // images x 12 heads x 1024 tokens) 531 -> 485 us in the same run,
-  // bit-identical (each 16-query tile takes the same steps in every form)
+  // bit-identical (each 16-query tile takes the same steps in every form).
+  // Q / K remainders (RoPE'd layers: masked or short-key ranges) take the
+  // checked kernel with 16 rows per wave (with 32 the remainder fragments
+  // push it past 256 VGPRs).
   const long g2 = (long)((sq + BQ<2> - 1) / BQ<2>) * hq * batch;
   const long g4 = (long)((sq + BQ<4> - 1) / BQ<4>) * hq * batch;
-  const bool qt1 = sq <= BQ<1> || g2 < 2 * kAttnCUs;
-  const bool full = mask_kind == SVLA_MASK_NONE && sk % BKEY == 0;
+  const bool qt1 = sq <= BQ<1> || g2 < 2 * kAttnCUs || lo > 0;
+  const bool full = mask_kind == SVLA_MASK_NONE && sk % BKEY == 0 && lo == 0;
   hipStream_t s = (hipStream_t)stream;
   if (qt1) {
     dim3 grid((sq + BQ<1> - 1) / BQ<1>, hq, batch);
-    if (full) hipLaunchKernelGGL((attention_kernel<true, 1>), grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((attention_kernel<false, 1>), grid, dim3(256), 0, s, p);
+    if (full) hipLaunchKernelGGL((attention_kernel<true, 1, 0>), grid, dim3(256), 0, s, p);
+    else if (lo == 0) hipLaunchKernelGGL((attention_kernel<false, 1, 0>), grid, dim3(256), 0, s, p);
+    else if (lo == 1) hipLaunchKernelGGL((attention_kernel<false, 1, 1>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((attention_kernel<false, 1, 2>), grid, dim3(256), 0, s, p);
   } else if (full && g4 >= 2 * kAttnCUs) {
     dim3 grid((sq + BQ<4> - 1) / BQ<4>, hq, batch);
-    hipLaunchKernelGGL((attention_kernel<true, 4>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((attention_kernel<true, 4, 0>), grid, dim3(256), 0, s, p);
   } else {
     dim3 grid((sq + BQ<2> - 1) / BQ<2>, hq, batch);
-    if (full) hipLaunchKernelGGL((attention_kernel<true, 2>), grid, dim3(256), 0, s, p);
-    else hipLaunchKernelGGL((attention_kernel<false, 2>), grid, dim3(256), 0, s, p);
+    if (full) hipLaunchKernelGGL((attention_kernel<true, 2, 0>), grid, dim3(256), 0, s, p);
+    else hipLaunchKernelGGL((attention_kernel<false, 2, 0>), grid, dim3(256), 0, s, p);
   }
   SVLA_CHECK_LAUNCH();
   return SVLA_OK;
+}
+
+extern "C" int svla_attention_bf16(const void* q, int ldq, long q_bs, const void* k, int ldk,
+                                   long k_bs, const void* v, int ldv, long v_bs, void* o, int ldo,
+                                   long o_bs, int batch, int sq, int sk, int hq, int hkv,
+                                   int head_dim, float scale, int mask_kind, int prefix_len,
+                                   svla_stream_t stream) {
+  return svla_attention_lo_bf16(q, nullptr, ldq, q_bs, k, nullptr, ldk, k_bs, v, ldv, v_bs, o,
+                                ldo, o_bs, batch, sq, sk, hq, hkv, head_dim, scale, mask_kind,
+                                prefix_len, stream);
 }

@@ -70,6 +70,7 @@ struct GemmArgs {
   const float* rope_sin;
   int rope_cols;
   int rope_period;
+  bf16* c_lo;  // ROPE (optional): o - bf16(o) of every rotated column, layout of c
   float* x_f32;
   long ldx;
   bf16* x_bf16;
@@ -224,6 +225,19 @@ __device__ __forceinline__ void epi_apply(const GemmArgs& p, int m, int n, float
     }
     store_bf16x4(c + n, o1);
     store_bf16x4(c + n + 32, o2);
+    if (p.c_lo && rot) {
+      // the reference scores the fp32 RoPE output: keep what bf16 drops
+      // (exact in fp32), so the attention can take Q = hi + lo
+      float l1[4], l2[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        l1[i] = __fsub_rn(o1[i], rbf(o1[i]));
+        l2[i] = __fsub_rn(o2[i], rbf(o2[i]));
+      }
+      bf16* cl = p.c_lo + crow(p, m) * p.ldc;
+      store_bf16x4(cl + n, l1);
+      store_bf16x4(cl + n + 32, l2);
+    }
   } else if constexpr (EPI == EPI_SILU) {
     // gate at packed column n (first half of a 64-block), up at n + 32; output
     // column (n / 64) * 32 + n % 64; out = bf16(bf16(silu(bf16(g))) * bf16(u))
@@ -2640,20 +2654,30 @@ int svla_slab_block_bf16(const void* x, int ldx, void* out, int rows, int k, svl
   return SVLA_OK;
 }
 
-int svla_linear_rope_bf16(const void* a, int lda, const void* w, int ldw, void* c, int ldc,
-                          int m, int n, int k, int rope_cols, int seq_len, const float* cos_t,
-                          const float* sin_t, const void* norm_w, float norm_eps,
-                          svla_stream_t stream) {
+int svla_linear_rope_lo_bf16(const void* a, int lda, const void* w, int ldw, void* c,
+                             void* c_lo, int ldc, int m, int n, int k, int rope_cols, int seq_len,
+                             const float* cos_t, const float* sin_t, const void* norm_w,
+                             float norm_eps, svla_stream_t stream) {
   if (!cos_t || !sin_t || rope_cols > n) return SVLA_EINVAL;
   if (!svla_aligned16(cos_t) || !svla_aligned16(sin_t)) return SVLA_EINVAL;
+  if (c_lo && ((uintptr_t)c_lo & 7)) return SVLA_EINVAL;
   GemmArgs p = base_args(a, lda, w, ldw, c, ldc, m, n, k);
   p.rope_cos = cos_t;
   p.rope_sin = sin_t;
   p.rope_cols = rope_cols;
   p.rope_period = seq_len;
+  p.c_lo = static_cast<bf16*>(c_lo);
   p.norm_w = static_cast<const bf16*>(norm_w);
   p.norm_eps = norm_eps;
   return run_gemm<A_DENSE>(p, EPI_ROPE, 0, (hipStream_t)stream);
+}
+
+int svla_linear_rope_bf16(const void* a, int lda, const void* w, int ldw, void* c, int ldc,
+                          int m, int n, int k, int rope_cols, int seq_len, const float* cos_t,
+                          const float* sin_t, const void* norm_w, float norm_eps,
+                          svla_stream_t stream) {
+  return svla_linear_rope_lo_bf16(a, lda, w, ldw, c, nullptr, ldc, m, n, k, rope_cols, seq_len,
+                                  cos_t, sin_t, norm_w, norm_eps, stream);
 }
 
 int svla_linear_silu_mul_bf16(const void* a, int lda, const void* w_gu, int ldw, void* out,

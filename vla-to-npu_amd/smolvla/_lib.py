@@ -61,12 +61,16 @@ SIGNATURES = {
     "svla_linear_scratch_bf16": [_p, _i, _p, _i, _p, _p, _p, _i, _p, _i, _i, _i, _i, _f, _i, _i,
                                  _p, _f, _p],
     "svla_linear_rope_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _f, _p],
+    "svla_linear_rope_lo_bf16": [_p, _i, _p, _i, _p, _p, _i, _i, _i, _i, _i, _i, _p, _p, _p, _f,
+                                 _p],
     "svla_linear_silu_mul_bf16": [_p, _i, _p, _i, _p, _i, _i, _i, _i, _p, _f, _p],
     "svla_patch_embed_bf16": [_p, _p, _p, _p, _p, _i, _i, _i, _i, _i, _i, _p],
     "svla_connector_bf16": [_p, _p, _i, _p, _i, _i, _i, _i, _i, _i, _i, _i, _p],
     "svla_action_out_euler": [_p, _i, _p, _i, _p, _i, _p, _i, _i, _i, _i, _p, _f, _f, _p],
     "svla_attention_bf16": [_p, _i, _l, _p, _i, _l, _p, _i, _l, _p, _i, _l, _i, _i, _i, _i, _i,
                             _i, _f, _i, _i, _p],
+    "svla_attention_lo_bf16": [_p, _p, _i, _l, _p, _p, _i, _l, _p, _i, _l, _p, _i, _l, _i, _i, _i,
+                               _i, _i, _i, _f, _i, _i, _p],
     "svla_masked_softmax_bf16": [_p, _i, _p, _i, _i, _p],
     "svla_softmax": [_p, _p, _i, _i, _i, _i, _p],
     "svla_silu_bf16": [_p, _p, _l, _p],

@@ -76,10 +76,14 @@ def work(name, args, cfg, batch):
                        " +res" if res else "", " f32out" if out_f32 else ""])
         kind = "linear_wide" if name == "svla_linear_wide_bf16" else "linear"
         return "mfma", 2 * m * n * k, by, f"{kind} {m}x{n}x{k}{tag}"
-    if name == "svla_linear_rope_bf16":
-        m, n, k = a[6], a[7], a[8]
-        by = 2 * (m * k + n * k + m * n) + (2 * k if a[13] else 0)
-        return "mfma", 2 * m * n * k, by, f"linear+rope {m}x{n}x{k}{' norm' if a[13] else ''}"
+    if name in ("svla_linear_rope_bf16", "svla_linear_rope_lo_bf16"):
+        lo = name == "svla_linear_rope_lo_bf16"
+        m, n, k = (a[7], a[8], a[9]) if lo else (a[6], a[7], a[8])
+        norm, rc = (a[14], a[10]) if lo else (a[13], a[9])
+        has_lo = lo and bool(a[5])
+        by = 2 * (m * k + n * k + m * n) + (2 * k if norm else 0) + (2 * m * rc if has_lo else 0)
+        return ("mfma", 2 * m * n * k, by,
+                f"linear+rope {m}x{n}x{k}{' norm' if norm else ''}{' +lo' if has_lo else ''}")
     if name == "svla_linear_silu_mul_bf16":
         m, inter, k = a[6], a[7], a[8]
         by = 2 * (m * k + 2 * inter * k + m * inter) + (2 * k if a[9] else 0)
@@ -100,12 +104,18 @@ def work(name, args, cfg, batch):
         m, n, k = a[8], a[9], a[10]
         by = 2 * (m * k + n * k) + 10 * m * n
         return "mfma", 2 * m * n * k, by, f"action out+euler {m}x{n}x{k}"
-    if name == "svla_attention_bf16":
-        b, sq, sk, hq, hkv, hd, mask = a[12], a[13], a[14], a[15], a[16], a[17], a[19]
+    if name in ("svla_attention_bf16", "svla_attention_lo_bf16"):
+        if name == "svla_attention_lo_bf16":
+            b, sq, sk, hq, hkv, hd, mask = a[14], a[15], a[16], a[17], a[18], a[19], a[21]
+            nlo = bool(a[1]) + bool(a[5])
+        else:
+            b, sq, sk, hq, hkv, hd, mask = a[12], a[13], a[14], a[15], a[16], a[17], a[19]
+            nlo = 0
         by = 2 * b * (2 * sq * hq * hd + 2 * sk * hkv * hd)
+        by += 2 * b * ((sq * hq * hd if nlo >= 1 else 0) + (sk * hkv * hd if nlo == 2 else 0))
         what = {0: "full", 1: "causal", 2: "prefix"}.get(mask, f"mask{mask}")
         return ("mfma", 4 * b * hq * sq * sk * hd, by,
-                f"attention b{b} {sq}x{sk} {hq}/{hkv} heads {what}")
+                f"attention b{b} {sq}x{sk} {hq}/{hkv} heads {what}{' +lo' * nlo}")
     if name == "svla_expert_run":
         steps = cfg.num_steps
         by = steps * expert_step_weight_bytes(cfg)

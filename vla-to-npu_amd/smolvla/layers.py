@@ -5,17 +5,18 @@ Weights are prepared once into the packed layouts the kernels consume
 current stream, writing into caller-provided buffers so a whole chunk can be
 captured in one HIP graph.  Activations are row-major ``[B*S, H]`` bf16.
 
-Per decoder layer (vla/text_encoder_bf16.py:480-595 -> 5 launches):
-  [RMSNorm -> QKV GEMM -> RoPE] -> fused GQA attention -> [O GEMM + residual]
-  -> [RMSNorm -> gate|up GEMM -> SiLU*up] -> [down GEMM + residual]
-(brackets = one kernel: the GEMM multiplies its A fragments by the norm gain,
-sums their squares on the way into the MFMAs and scales each row by 1 / rms in
-the epilogue).  The fusion saves a launch and a pass over x, and costs VALU
-work inside the GEMM, which only pays up to M = FUSED_NORM_MAX_ROWS (measured
-on MI355X, in-graph: expert at batch 32, M = 1600, gate|up 22.9 us fused vs
-24.2 us norm + GEMM, QKV 20.5 vs 20.4; prefix at batch 32, M = 7712, gate|up
-129.8 vs 111.1, QKV 60.4 vs 57.8); above it the norm runs as its own kernel
-(7 launches per layer).
+Per decoder layer (vla/text_encoder_bf16.py:480-595 -> 7 launches):
+  RMSNorm -> [QKV GEMM -> RoPE] -> fused GQA attention -> [O GEMM + residual]
+  -> RMSNorm -> [gate|up GEMM -> SiLU*up] -> [down GEMM + residual]
+(brackets = one kernel).  The RMSNorm runs as its own bandwidth kernel, which
+rounds once, bf16(x * (1/rms) * gain), as torch's bf16 RMSNorm does; the
+GEMMs can also fuse the norm into their A path (``norm=``), but then round
+bf16(x * gain) and scale by 1/rms in the epilogue, a different rounding point
+that moves a layer output by up to ~1e-2 relative on real activations, so the
+layers here do not use it (measured on MI355X it saved at most ~1.3 us per
+norm: expert at batch 32, M = 1600, gate|up 22.9 us fused vs 24.2 us).  RoPE'd
+Q and K also carry their bf16 remainders into the attention, which then scores
+the fp32 values as the reference module does.
 """
 
 from __future__ import annotations
@@ -173,8 +174,9 @@ class Buffers:
 
 
 # ----------------------------------------------------------------- layers ---
-# fuse the RMSNorm into the consuming GEMM up to this many rows (see above)
-FUSED_NORM_MAX_ROWS = 2048
+# fuse the RMSNorm into the consuming GEMM up to this many rows; 0: never
+# (the standalone kernel keeps the reference's single rounding, see above)
+FUSED_NORM_MAX_ROWS = 0
 
 
 def _normed(x, w, eps, M, bufs, name):
@@ -197,12 +199,17 @@ def decoder_layer(x, P, cfg: DecoderConfig, B, L, rope: Rope, mask="causal", pre
     qd, kvd = cfg.q_dim, cfg.kv_dim
     eps = resolve_eps(cfg.rms_eps)
     qkv = qkv_out if qkv_out is not None else bufs.get("qkv", M, qd + 2 * kvd)
+    # remainders of the fp32 post-RoPE Q and K, which the reference module
+    # scores in fp32 (vla/text_encoder_bf16.py:92-104, 117-122); the cache
+    # keeps the bf16 values (:595)
+    lo = bufs.get("qkv_lo", M, qkv.stride(0))[:, :qd + 2 * kvd]
     a, nrm = _normed(x, P["n1"], eps, M, bufs, "xn")
-    ops.linear_rope(a, P["wqkv"], qd + kvd, L, rope.cos, rope.sin, out=qkv, norm=nrm)
-    q3 = qkv.view(B, L, -1)
+    ops.linear_rope(a, P["wqkv"], qd + kvd, L, rope.cos, rope.sin, out=qkv, norm=nrm, out_lo=lo)
+    q3, l3 = qkv.view(B, L, -1), lo.view(B, L, -1)
     attn = bufs.get("attn", M, qd)
     ops.attention(q3[:, :, :qd], q3[:, :, qd:qd + kvd], q3[:, :, qd + kvd:],
-                  attn.view(B, L, qd), cfg.n_q_heads, cfg.n_kv_heads, mask, prefix_len)
+                  attn.view(B, L, qd), cfg.n_q_heads, cfg.n_kv_heads, mask, prefix_len,
+                  q_lo=l3[:, :, :qd], k_lo=l3[:, :, qd:qd + kvd])
     ops.linear(attn, P["wo"], res=x, out=x)
     if mid_out is not None:
         mid_out.copy_(x)
@@ -254,11 +261,12 @@ def cross_layer(x, ck, cv, P, cfg: DecoderConfig, B, L, Lc, rope: Rope,
     qd = cfg.q_dim
     eps = resolve_eps(cfg.rms_eps)
     a, nrm = _normed(x, P["n1"], eps, M, bufs, "xn")
+    q_lo = bufs.get("q_lo", M, qd)
     q = ops.linear_rope(a, P["wq"], qd, L, rope.cos, rope.sin, out=bufs.get("q", M, qd),
-                        norm=nrm)
+                        norm=nrm, out_lo=q_lo)
     attn = bufs.get("attn", M, qd)
     ops.attention(q.view(B, L, qd), ck.view(B, Lc, -1), cv.view(B, Lc, -1), attn.view(B, L, qd),
-                  cfg.n_q_heads, cfg.n_kv_heads, "none", 0)
+                  cfg.n_q_heads, cfg.n_kv_heads, "none", 0, q_lo=q_lo.view(B, L, qd))
     ops.linear(attn, P["wo"], res=x, out=x)
     _mlp(x, P, cfg, M, eps, bufs)
 

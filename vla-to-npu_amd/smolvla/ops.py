@@ -238,13 +238,20 @@ def linear_wide(a, w, m, n, k, bias=None, bias_f32=None, res=None, act=None, alp
     return out
 
 
-def linear_rope(a, w, rope_cols, seq_len, cos_t, sin_t, out=None, norm=None):
+def linear_rope(a, w, rope_cols, seq_len, cos_t, sin_t, out=None, norm=None, out_lo=None):
+    """QKV projection with RoPE on the first ``rope_cols`` columns;
+    ``out_lo`` (optional, the shape and row stride of ``out``) receives the
+    bf16 remainder of each rotated column's fp32 value
+    (``svla_linear_rope_lo_bf16``)."""
     M, K = a.shape
     N = w.shape[0]
     out = torch.empty(M, N, dtype=BF16, device=a.device) if out is None else out
     nw, ne = _norm_args(norm)
-    _lib.call("svla_linear_rope_bf16", _ptr(a), _ld(a), _ptr(w), _ld(w), _ptr(out), _ld(out), M,
-              N, K, rope_cols, seq_len, _ptr(cos_t), _ptr(sin_t), nw, ne, _stream())
+    if out_lo is not None and (out_lo.shape != out.shape or _ld(out_lo) != _ld(out)):
+        raise ValueError("linear_rope: out_lo must have out's shape and row stride")
+    _lib.call("svla_linear_rope_lo_bf16", _ptr(a), _ld(a), _ptr(w), _ld(w), _ptr(out),
+              _ptr(out_lo), _ld(out), M, N, K, rope_cols, seq_len, _ptr(cos_t), _ptr(sin_t), nw,
+              ne, _stream())
     return out
 
 
@@ -297,19 +304,27 @@ def action_out_euler(a, w, x_f32, dt, x_bf16=None, norm=None):
 
 
 # ------------------------------------------------------------- attention ---
-def attention(q, k, v, out, hq, hkv, mask="causal", prefix_len=0, scale=None):
+def attention(q, k, v, out, hq, hkv, mask="causal", prefix_len=0, scale=None, q_lo=None,
+              k_lo=None):
     """``q [B, Sq, >=hq*64]``, ``k``/``v [B, Sk, >=hkv*64]`` (views into fused
-    projection buffers are fine: row stride = ``stride(1)``), ``out [B, Sq, hq*64]``."""
+    projection buffers are fine: row stride = ``stride(1)``), ``out [B, Sq, hq*64]``.
+    ``q_lo`` / ``k_lo``: bf16 remainders of fp32 Q / K (views with q's / k's
+    strides, from :func:`linear_rope`'s ``out_lo``): the scores are then taken
+    on Q = q + q_lo, K = k + k_lo (``svla_attention_lo_bf16``)."""
     B, Sq = q.shape[0], q.shape[1]
     Sk = k.shape[1]
     for t in (q, k, v, out):
         if t.dim() != 3 or t.stride(-1) != 1:
             raise ValueError("attention takes [B, S, H*D] row-major views")
+    for lo, hi in ((q_lo, q), (k_lo, k)):
+        if lo is not None and (lo.shape != hi.shape or lo.stride() != hi.stride()):
+            raise ValueError("attention: a remainder needs its operand's shape and strides")
     scale = 1.0 / math.sqrt(64) if scale is None else scale
-    _lib.call("svla_attention_bf16",
-              _ptr(q), q.stride(1), q.stride(0), _ptr(k), k.stride(1), k.stride(0),
-              _ptr(v), v.stride(1), v.stride(0), _ptr(out), out.stride(1), out.stride(0),
-              B, Sq, Sk, hq, hkv, 64, float(scale), MASK[mask], int(prefix_len), _stream())
+    _lib.call("svla_attention_lo_bf16",
+              _ptr(q), _ptr(q_lo), q.stride(1), q.stride(0), _ptr(k), _ptr(k_lo), k.stride(1),
+              k.stride(0), _ptr(v), v.stride(1), v.stride(0), _ptr(out), out.stride(1),
+              out.stride(0), B, Sq, Sk, hq, hkv, 64, float(scale), MASK[mask], int(prefix_len),
+              _stream())
     return out
 
 

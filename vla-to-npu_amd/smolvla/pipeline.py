@@ -219,8 +219,11 @@ class SmolVLAEngine:
             else:
                 layers.decoder_layer(self.ex, P, e, B, L, self.rope_expert, "causal", 0,
                                      self.ebufs)
-        ops.action_out_euler(self.ex, self.w_aout, self.x_t, dt, x_bf16=self.x_bf,
-                             norm=(self.n_exp, resolve_eps(e.rms_eps)))
+        # final expert RMSNorm (one rounding, as torch's) then action_out + Euler
+        # (vla/vla.py:218-222)
+        h = ops.rmsnorm(self.ex, self.n_exp, resolve_eps(e.rms_eps),
+                        out=self.ebufs.get("xn_out", B * L, e.hidden))
+        ops.action_out_euler(h, self.w_aout, self.x_t, dt, x_bf16=self.x_bf)
 
     def _forward(self):
         cfg = self.cfg
