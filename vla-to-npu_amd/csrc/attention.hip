@@ -529,6 +529,155 @@ __global__ __launch_bounds__(256, 2) void attention_kernel(AttnArgs p) {
   }
 }
 
+// Exact attention for short key ranges (sk <= 64 NB: the RoPE'd layers' 50
+// and 241 keys), single pass: the K rows (and their remainders, LO == 2) and
+// V rows of the (sample, KV head) are staged into LDS once, every score of a
+// query stays in registers (NB blocks x 4 subtiles), so the maximum, the fp32
+// sum l = sum exp(s - m) and p = bf16(exp(s - m) * (1 / l)) -- torch's
+// softmax(...).to(bf16) -- come without a second pass over K.  Wave w of the
+// workgroup takes query tile (16 rows) blockIdx.x * qtiles + w % qtiles of
+// head blockIdx.y * hpw + w / qtiles; the hpw heads share one KV head, whose
+// K / V are then staged once for all of them.  LO as for attention_kernel
+// (1: Q = q + q_lo; 2: also K = k + k_lo).
+constexpr int SHORT_KEYS = 256;
+template <int LO, int NB>
+__global__ __launch_bounds__(1024, 1) void attention_short_kernel(AttnArgs p, int hpw, int qtiles) {
+  constexpr int KLO = LO == 2 ? NB * BKEY * D : 64;
+  __shared__ __attribute__((aligned(1024))) bf16 sK[NB * BKEY * D];
+  __shared__ __attribute__((aligned(1024))) bf16 sV[NB * BKEY * D];
+  __shared__ __attribute__((aligned(1024))) bf16 sL[KLO];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nw = blockDim.x >> 6;
+  const int h = blockIdx.y * hpw + wave / qtiles, b = blockIdx.z;
+  const int kvh = blockIdx.y * hpw * p.hkv / p.hq;
+  const int q0 = blockIdx.x * qtiles * 16;
+  const int grp = lane >> 4, col = lane & 15;
+  const int qi = q0 + (wave % qtiles) * 16 + col;           // this lane's query row
+
+  // keys any row of this workgroup may see
+  int kend = p.sk;
+  if (p.mask_kind != SVLA_MASK_NONE) {
+    int lim = min(p.sq, q0 + qtiles * 16);
+    if (p.mask_kind == SVLA_MASK_PREFIX_LM) lim = max(lim, p.prefix_len);
+    kend = min(kend, lim);
+  }
+  const int nb = (kend + BKEY - 1) / BKEY;                   // <= NB (launcher)
+
+  // stage K (+ K_lo) and V rows 0 .. 64 nb - 1 (clamped to sk - 1): one 1 KB
+  // DMA instruction per 8 rows, dealt round the waves; chunk c of key row r
+  // at slot c ^ (r & 7) (kv_off)
+  {
+    const bf16* kb = p.k + b * p.k_bs + kvh * D;
+    const bf16* vb = p.v + b * p.v_bs + kvh * D;
+    const bf16* lb = LO == 2 ? p.k_lo + b * p.k_bs + kvh * D : nullptr;
+    const int n8 = nb * (BKEY / 8);
+    for (int i = wave; i < n8; i += nw) {
+      const int key = i * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ (key & 7);
+      const long kr = min(key, p.sk - 1);
+      __builtin_amdgcn_global_load_lds((void*)(kb + kr * p.ldk + c * 8), (lds_ptr_t)(sK + i * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((void*)(vb + kr * p.ldv + c * 8), (lds_ptr_t)(sV + i * 512), 16, 0, 0);
+      if constexpr (LO == 2)
+        __builtin_amdgcn_global_load_lds((void*)(lb + kr * p.ldk + c * 8), (lds_ptr_t)(sL + i * 512), 16, 0, 0);
+    }
+  }
+  // Q fragments (B operand of S^T), rows clamped (never stored past sq)
+  const int qc = min(qi, p.sq - 1);
+  const long qoff = b * p.q_bs + h * D + (long)qc * p.ldq;
+  bf16x8 qf[2], qlf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    qf[ks] = ld8(p.q + qoff + ks * 32 + grp * 8);
+    if constexpr (LO >= 1) qlf[ks] = ld8(p.q_lo + qoff + ks * 32 + grp * 8);
+  }
+  const int klim = key_limit(p.mask_kind, qi, p.sk, p.prefix_len);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  // S^T for every key block: s[blk][ts] lane holds keys 64 blk + 16 ts + 4 grp + i
+  f32x4 s[NB][4];
+#pragma unroll
+  for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts) {
+      f32x4 a = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      if (blk < nb) {  // uniform
+        a = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int off = kv_off(blk * BKEY + ts * 16 + col, ks * 32 + grp * 8);
+          const bf16x8 kf = *reinterpret_cast<const bf16x8*>(&sK[off]);
+          if constexpr (LO == 2)
+            a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(&sL[off]),
+                                                        qf[ks], a, 0, 0, 0);
+          if constexpr (LO >= 1) a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qlf[ks], a, 0, 0, 0);
+          a = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[ks], a, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (blk * BKEY + ts * 16 + grp * 4 + i >= klim) a[i] = -INFINITY;
+      }
+      s[blk][ts] = a;
+    }
+  const float c = p.scale_log2;
+  float mx = s[0][0][0];
+#pragma unroll
+  for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = smax(mx, s[blk][ts][i]);
+  mx = max_xor32(max_xor16(mx));                   // finite: key 0 is always visible
+  const float off = -(mx * c);
+  float l = 0.f;
+#pragma unroll
+  for (int blk = 0; blk < NB; ++blk)
+#pragma unroll
+    for (int ts = 0; ts < 4; ++ts)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[blk][ts][i], c, off));
+        s[blk][ts][i] = e;
+        l += e;
+      }
+  l = sum_xor32(sum_xor16(l));
+  const float rl = 1.0f / l;
+  // O^T[d, q] += V^T[d, keys] . P^T[keys, q], p = bf16(e / l)
+  f32x4 o[4];
+#pragma unroll
+  for (int td = 0; td < 4; ++td) o[td] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int blk = 0; blk < NB; ++blk) {
+    if (blk >= nb) break;  // uniform
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf16x8 pf;
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pf[hh * 4 + i] = f2bf(s[blk][2 * kk + hh][i] * rl);
+#pragma unroll
+      for (int td = 0; td < 4; ++td) {
+        const v4i16 lo = v_tr_read(sV, blk * BKEY + kk * 32 + 4 * grp, td * 16, col);
+        const v4i16 hi = v_tr_read(sV, blk * BKEY + kk * 32 + 16 + 4 * grp, td * 16, col);
+        const v4i16 w8[2] = {lo, hi};
+        o[td] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(*reinterpret_cast<const bf16x8*>(w8), pf,
+                                                        o[td], 0, 0, 0);
+      }
+    }
+  }
+  if (qi >= p.sq) return;
+  bf16* orow = p.o + b * p.o_bs + (long)qi * p.ldo + h * D;
+#pragma unroll
+  for (int td = 0; td < 4; ++td) {
+    bf16x4 r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = f2bf(o[td][i]);
+    *reinterpret_cast<bf16x4*>(orow + td * 16 + grp * 4) = r;
+  }
+}
+
 }  // namespace
 
 extern "C" int svla_attention_lo_bf16(const void* q, const void* q_lo, int ldq, long q_bs,
@@ -576,6 +725,29 @@ extern "C" int svla_attention_lo_bf16(const void* q, const void* q_lo, int ldq, 
   const bool qt1 = sq <= BQ<1> || g2 < 2 * kAttnCUs || lo > 0;
   const bool full = mask_kind == SVLA_MASK_NONE && sk % BKEY == 0 && lo == 0;
   hipStream_t s = (hipStream_t)stream;
+  if (lo > 0 && sk <= SHORT_KEYS) {
+    // RoPE'd layers: the single-pass exact form.  Up to 64 queries (the
+    // expert): one workgroup per (sample, KV head) holding all its query
+    // heads (hpw = hq / hkv, 4 query tiles each) when that fits 16 waves;
+    // longer ranges (the prefix): one head, up to 16 query tiles (256 rows).
+    const int tiles = (sq + 15) / 16;
+    int hpw = 1, qtiles = min(tiles, 16);
+    if (tiles <= 4 && (hq / hkv) * tiles <= 16) {
+      hpw = hq / hkv;
+      qtiles = tiles;
+    }
+    dim3 grid((tiles + qtiles - 1) / qtiles, hq / hpw, batch);
+    const dim3 block(64 * hpw * qtiles);
+    if (sk <= BKEY) {
+      if (lo == 1) hipLaunchKernelGGL((attention_short_kernel<1, 1>), grid, block, 0, s, p, hpw, qtiles);
+      else hipLaunchKernelGGL((attention_short_kernel<2, 1>), grid, block, 0, s, p, hpw, qtiles);
+    } else {
+      if (lo == 1) hipLaunchKernelGGL((attention_short_kernel<1, 4>), grid, block, 0, s, p, hpw, qtiles);
+      else hipLaunchKernelGGL((attention_short_kernel<2, 4>), grid, block, 0, s, p, hpw, qtiles);
+    }
+    SVLA_CHECK_LAUNCH();
+    return SVLA_OK;
+  }
   if (qt1) {
     dim3 grid((sq + BQ<1> - 1) / BQ<1>, hq, batch);
     if (full) hipLaunchKernelGGL((attention_kernel<true, 1, 0>), grid, dim3(256), 0, s, p);
