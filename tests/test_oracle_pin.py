@@ -671,3 +671,123 @@ def test_expert_velocity_routes_cross_layer_kv(fp32_probs):
         h = h0 + (ctx @ _d(Q["expert"][live]["Wo"]))[:, None, :]
         want = ref.expert_output(h.float(), Q, cfg)
         assert torch.allclose(got, want, atol=1e-4), live
+
+
+# --------------------------------------------------------------------------
+# stack-level pins: the oracle's vision_encoder and prefix_forward against
+# transformers' own stacks (local configs, loaded with the same weights)
+def _llama_sd(p, prefix=""):
+    sd = {
+        "self_attn.q_proj.weight": p["Wq"].t(), "self_attn.k_proj.weight": p["Wk"].t(),
+        "self_attn.v_proj.weight": p["Wv"].t(), "self_attn.o_proj.weight": p["Wo"].t(),
+        "mlp.gate_proj.weight": p["W_gate"].t(), "mlp.up_proj.weight": p["W_up"].t(),
+        "mlp.down_proj.weight": p["W_down"].t(),
+        "input_layernorm.weight": p["W_norm_1"], "post_attention_layernorm.weight": p["W_norm_2"],
+    }
+    return {prefix + k: v.float().contiguous() for k, v in sd.items()}
+
+
+def test_prefix_forward_matches_transformers_llama_stack(fp32_probs):
+    """``prefix_forward`` (16 decoder layers with the prefix-LM mask, per-layer
+    K/V cache) against a 2-layer transformers ``LlamaModel`` fed the same
+    embeddings with the prefix-LM 4-D mask: every layer's output (forward
+    hooks) and every layer's post-RoPE K and V (the model's own cache).  A
+    causal mask, or the K/V of the neighbouring layer, fails the comparison."""
+    from transformers import LlamaConfig, LlamaModel
+    dc = DecoderConfig()
+    L, bidir = 41, 40                      # 40 bidirectional tokens, 1 causal state token
+    cfg = types.SimpleNamespace(decoder=dc, prefix_mask="prefix_lm", prefix_bidir_len=bidir)
+    gen = _Gen(40, norm_init="random")
+    layers = [to32(decoder_layer_params(gen, dc)) for _ in range(2)]
+    x = torch.randn(1, L, dc.hidden, generator=torch.Generator().manual_seed(41))
+    lc = LlamaConfig(hidden_size=dc.hidden, intermediate_size=dc.inter,
+                     num_attention_heads=dc.n_q_heads, num_key_value_heads=dc.n_kv_heads,
+                     head_dim=dc.head_dim, num_hidden_layers=2, rope_theta=dc.rope_theta,
+                     rms_norm_eps=dc.rms_eps, vocab_size=16, max_position_embeddings=512,
+                     attention_bias=False, mlp_bias=False, hidden_act="silu")
+    lc._attn_implementation = "eager"
+    model = LlamaModel(lc).eval()
+    sd = {}
+    for i, p in enumerate(layers):
+        sd.update(_llama_sd(p, f"layers.{i}."))
+    missing, unexpected = model.load_state_dict(sd, strict=False)
+    assert not unexpected and all(not k.startswith("layers.") for k in missing)
+    outs = []
+    hooks = [m.register_forward_hook(lambda mod, a, o: outs.append(o[0] if isinstance(o, tuple) else o))
+             for m in model.layers]
+
+    def run_llama(mask_bool):
+        outs.clear()
+        add = torch.zeros(1, 1, L, L).masked_fill(mask_bool, float("-inf"))
+        with torch.no_grad():
+            r = model(inputs_embeds=x, attention_mask=add, use_cache=True)
+        cache = r.past_key_values
+        kv = [(cache.layers[i].keys, cache.layers[i].values) for i in range(2)]
+        return list(outs), kv
+
+    with torch.no_grad():
+        got_x, got_kv = ref.prefix_forward(x, {"prefix": layers}, cfg)
+    hl, kvl = run_llama(ref.make_mask("prefix_lm", L, L, bidir))
+    for h in hooks:
+        h.remove()
+    assert torch.allclose(got_x, hl[1], atol=5e-4, rtol=1e-3), (got_x - hl[1]).abs().max()
+    to_bhld = lambda t: t.view(1, L, dc.n_kv_heads, dc.head_dim).transpose(1, 2)  # noqa: E731
+    for i in range(2):
+        k, v = got_kv[i]
+        assert torch.allclose(to_bhld(k), kvl[i][0], atol=2e-4, rtol=1e-3), i
+        assert torch.allclose(to_bhld(v), kvl[i][1], atol=2e-4, rtol=1e-3), i
+    # sensitivity: the neighbouring layer's K, and a causal mask, do not match
+    assert not torch.allclose(to_bhld(got_kv[0][0]), kvl[1][0], atol=1e-2)
+    hooks = [m.register_forward_hook(lambda mod, a, o: outs.append(o[0] if isinstance(o, tuple) else o))
+             for m in model.layers]
+    hc, _ = run_llama(ref.make_mask("causal", L, L))
+    for h in hooks:
+        h.remove()
+    assert not torch.allclose(got_x, hc[1], atol=1e-2)
+
+
+def test_vision_encoder_matches_siglip_embeddings_and_encoder():
+    """``vision_encoder`` (patch embedding + position table, then the ViT
+    blocks, no post-LayerNorm) against transformers' ``SiglipVisionEmbeddings``
+    followed by a 2-layer ``SiglipEncoder`` on the same weights, for two
+    cameras of two samples (the [B, C, N, E] layout)."""
+    from transformers.models.siglip.modeling_siglip import SiglipEncoder, SiglipVisionEmbeddings
+    vc = VitConfig(image=64, layers=2)
+    gen = _Gen(42, norm_init="random")
+    vit = [to32(vit_layer_params(gen, vc)) for _ in range(2)]
+    kernel, bias = gen.randn(768, 3, 16, 16).float() * 0.05, gen.randn(768).float() * 0.02
+    pos = gen.randn(16, 768).float() * 0.02
+    params = {"patch": {"kernel": kernel, "bias": bias, "pos_emb": pos}, "vit": vit}
+    sc = _siglip(vc)
+    sc.num_hidden_layers = 2
+    emb = SiglipVisionEmbeddings(sc).eval()
+    emb.load_state_dict({"patch_embedding.weight": kernel, "patch_embedding.bias": bias,
+                         "position_embedding.weight": pos}, strict=False)
+    enc = SiglipEncoder(sc).eval()
+    sd = {}
+    for i, p in enumerate(vit):
+        pre = f"layers.{i}."
+        sd.update({
+            pre + "self_attn.q_proj.weight": p["Wq"].t(), pre + "self_attn.q_proj.bias": p["bq"],
+            pre + "self_attn.k_proj.weight": p["Wk"].t(), pre + "self_attn.k_proj.bias": p["bk"],
+            pre + "self_attn.v_proj.weight": p["Wv"].t(), pre + "self_attn.v_proj.bias": p["bv"],
+            pre + "self_attn.out_proj.weight": p["Wo"].t(), pre + "self_attn.out_proj.bias": p["bo"],
+            pre + "mlp.fc1.weight": p["W_up"].t(), pre + "mlp.fc1.bias": p["b_up"],
+            pre + "mlp.fc2.weight": p["W_down"].t(), pre + "mlp.fc2.bias": p["b_down"],
+            pre + "layer_norm1.weight": p["W_norm_1"], pre + "layer_norm1.bias": p["b_norm_1"],
+            pre + "layer_norm2.weight": p["W_norm_2"], pre + "layer_norm2.bias": p["b_norm_2"],
+        })
+    enc.load_state_dict({k: v.contiguous() for k, v in sd.items()})
+    images = torch.rand(2, 2, 3, 64, 64, generator=torch.Generator().manual_seed(43)) * 2 - 1
+    cfg = types.SimpleNamespace(vit=vc)
+    with torch.no_grad():
+        got = ref.vision_encoder(images, params, cfg)
+        want = enc(inputs_embeds=emb(images.reshape(4, 3, 64, 64))).last_hidden_state
+    assert got.shape == (2, 2, 16, 768)
+    assert torch.allclose(got.reshape(4, 16, 768), want, atol=5e-4, rtol=1e-3), \
+        (got.reshape(4, 16, 768) - want).abs().max()
+    # camera order: swapping two cameras of one sample moves exactly their tokens
+    sw = images[:, [1, 0]]
+    with torch.no_grad():
+        got_sw = ref.vision_encoder(sw, params, cfg)
+    assert torch.allclose(got_sw[:, 0], got[:, 1]) and torch.allclose(got_sw[:, 1], got[:, 0])
