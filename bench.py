@@ -530,6 +530,66 @@ def write_kernel_table(cfg, params, batch):
         f"{statistics.median(ts):.3f} ms per graph replay")
 
 
+def profile_chunks(cfg, params, batch, calls_out, eager_only):
+    """Profiler entry point (``--profile-chunks``): the libsvla calls of one
+    chunk at ``batch`` (with their work model and, unless ``eager_only``, the
+    census's isolated replay times) written to ``calls_out``; then the chunk
+    once more, as the last work of the process: three graph replays, or
+    (``eager_only``, for counter runs) one eager chunk."""
+    from smolvla import census
+    from smolvla.params import smolvla_inputs
+    from smolvla.pipeline import SmolVLAEngine
+    eng = SmolVLAEngine(cfg, params, batch=batch, use_graph=False)
+    eng.load_inputs(*smolvla_inputs(cfg, batch, seed=1, device="cuda"))
+    eng.step()
+    calls = census.record_chunk(eng)
+    iso = {}
+    if not eager_only:
+        for g in census.time_groups(census.group_calls(calls, cfg, batch)):
+            iso[g.label] = g.us
+    pathlib.Path(calls_out).write_text(json.dumps(
+        {"batch": batch, "calls": census.call_list(calls, cfg, batch), "iso_us": iso}))
+    if eager_only:
+        eng.step()
+    else:
+        eng.use_graph = True
+        eng.capture()
+        for _ in range(3):
+            eng.step()
+    torch.cuda.synchronize()
+    eng.check()
+    log(f"profile chunks at batch {batch}: {len(calls)} calls per chunk")
+
+
+def profile_summary(calls_json, trace_csv, pmc_csvs, out_md, trace_cmd, pmc_cmds):
+    """profiles/kernel_table_inchunk_bs<B>.md from a kernel-trace run and the
+    counter runs of ``--profile-chunks``."""
+    import csv
+    from smolvla import census
+    rec = json.loads(pathlib.Path(calls_json).read_text())
+    calls = [tuple(c) for c in rec["calls"]]
+    trace = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    pmc = [list(csv.DictReader(open(p))) for p in pmc_csvs]
+    rows, total_ms, n = census.profile_table(calls, rec["iso_us"], trace, pmc, rec["batch"])
+    cmds = "\n".join([trace_cmd] + pmc_cmds)
+    pathlib.Path(out_md).write_text(
+        f"# In-chunk kernel profile: one SmolVLA chunk at batch {rec['batch']}\n\n"
+        f"Commands (repo root on the MI355X box, `cd /tmp && export TMPDIR=/tmp` first, `R` = repo "
+        f"root; the counter runs one pass each):\n\n```\n{cmds}\n```\n\n"
+        f"The {n} library dispatches of the last graph-replayed chunk of the kernel trace are matched, "
+        f"in order, to the chunk's {len(calls)} libsvla calls (kernel families checked call by call) and "
+        f"grouped as the census groups them (entry point, shape, epilogue).  *isolated us*: the census's "
+        f"replay of the group alone in a graph; *in-chunk us*: the group's launches inside the replayed "
+        f"chunk (rocprofv3 kernel trace).  Peak fraction from the in-chunk time (2.5 PFLOP/s bf16 MFMA or "
+        f"8 TB/s HBM).  Counters per dispatch, averaged over the group's launches in one eager chunk of "
+        f"each counter run: *MFMA busy* = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE / 8 XCDs x 1024 SIMDs); "
+        f"*issuing* / *waiting* = SQ_ACTIVE_INST_ANY / SQ_WAIT_ANY over SQ_WAVE_CYCLES; *L2 hit* = "
+        f"TCC_HIT / (TCC_HIT + TCC_MISS); *fetched / algorithmic* = FETCH_SIZE x 1024 x "
+        f"{census.FETCH_SCALE:g} (the copy calibration) over the group's algorithmic bytes.\n\n"
+        f"Sum of in-chunk kernel time: {total_ms:.3f} ms per chunk.  Top 30 groups by time:\n\n{rows}\n")
+    log(f"wrote {out_md}: {n} dispatches, {total_ms:.3f} ms of kernel time")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -546,6 +606,18 @@ def main():
                     help="only launch the dominant kernel and a calibration copy (for rocprofv3 --pmc)")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
                     help="turn the two --traffic-probe counter CSVs into the committed record")
+    ap.add_argument("--profile-chunks", type=int, metavar="BATCH",
+                    help="profiler entry point: write one chunk's call list to --calls-out, then "
+                         "replay the chunk (run under rocprofv3)")
+    ap.add_argument("--calls-out", default="chunk_calls.json")
+    ap.add_argument("--eager-only", action="store_true",
+                    help="with --profile-chunks: end with one eager chunk (counter runs)")
+    ap.add_argument("--profile-summary", nargs="+", metavar="CSV",
+                    help="CALLS_JSON TRACE_CSV [PMC_CSV ...]: write --out from a --profile-chunks "
+                         "kernel trace and its counter runs")
+    ap.add_argument("--out", default=None)
+    ap.add_argument("--trace-cmd", default="")
+    ap.add_argument("--pmc-cmd", action="append", default=[])
     ap.add_argument("--kernel-table", type=int, metavar="BATCH",
                     help="only write the per-kernel census table of one chunk at this batch "
                          "to profiles/kernel_table_bs<BATCH>.md")
@@ -569,8 +641,15 @@ def main():
         traffic_summary(*args.traffic_summary,
                         (args.batch * cfg.n_cameras * v.tokens, v.inter, v.hidden))
         return
+    if args.profile_summary:
+        a = args.profile_summary
+        profile_summary(a[0], a[1], a[2:], args.out, args.trace_cmd, args.pmc_cmd)
+        return
     log("generating seeded random-init bf16 weights")
     params = smolvla_params(cfg, seed=0)
+    if args.profile_chunks:
+        profile_chunks(cfg, params, args.profile_chunks, args.calls_out, args.eager_only)
+        return
     if args.kernel_table:
         write_kernel_table(cfg, params, args.kernel_table)
         return

@@ -31,6 +31,12 @@ from . import _lib
 
 PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
+N_SIMD = 256 * 4            # MI355X: 256 CUs x 4 SIMDs
+N_XCD = 8                   # GRBM_GUI_ACTIVE reads the sum over the 8 XCDs
+# FETCH_SIZE (KiB) reads half the bytes a plain 1 GiB device copy moves on the
+# MI355X boxes measured (calibration committed with the dominant kernel's
+# traffic record): bytes = FETCH_SIZE x 1024 x FETCH_SCALE
+FETCH_SCALE = 2.0
 
 
 def _v(a):
@@ -265,3 +271,131 @@ def table(groups, top=25):
                     f"{100 * g.us * g.n / total:.1f} | {wk} | {ach:.1f} {unit} | "
                     f"{frac:.3f} ({'MFMA' if g.bound == 'mfma' else 'HBM'}) |")
     return "\n".join(rows), total / 1e3
+
+
+# ------------------------------------------------------------------------------
+# In-chunk profile: the kernels of one graph-replayed chunk, as a profiler sees
+# them, matched to the libsvla calls of the chunk (same order), so every census
+# group gets its in-chunk time and hardware counters beside its isolated replay.
+
+# kernel-name prefixes a call may dispatch, in order (one kernel per call
+# unless listed otherwise)
+_FAMILIES = {
+    "svla_linear_wide_bf16": [("gemm_wide_kernel",)],
+    "svla_attention_bf16": [("attention_",)],
+    "svla_attention_lo_bf16": [("attention_",)],
+    "svla_expert_run": [("clear_u32_kernel",), ("expert_kernel",)],
+    "svla_rmsnorm_bf16": [("rmsnorm_kernel",)],
+    "svla_layernorm_bf16": [("layernorm_kernel",)],
+    "svla_layernorm_blocked_bf16": [("layernorm_kernel",)],
+}
+_GEMM = ("gemm_", "skinny_kernel")
+
+
+def dispatch_families(name):
+    """Kernel-name prefixes of the dispatches one call makes, in order."""
+    if name in _FAMILIES:
+        return _FAMILIES[name]
+    if name.startswith(("svla_linear", "svla_patch", "svla_connector", "svla_action_out")):
+        return [_GEMM]
+    return [("",)]  # any one kernel
+
+
+def call_list(calls, cfg, batch):
+    """[(entry point, bound, flops, bytes, group label)] of recorded calls."""
+    return [(name, *work(name, args, cfg, batch)) for name, args in calls]
+
+
+def short_kernel_name(n):
+    """``void (anonymous namespace)::gemm_line_kernel<...>(GemmArgs)`` ->
+    ``gemm_line_kernel<...>``."""
+    import re
+    n = n.replace("void ", "").replace("(anonymous namespace)::", "")
+    return re.sub(r"\((?:[^()]|\([^()]*\))*\)$", "", n).strip()
+
+
+def own_dispatches(rows):
+    """Profiler rows of this library's kernels, in dispatch order: they live
+    in top-level anonymous namespaces (torch's kernels sit in named ones, the
+    runtime's copies in none)."""
+    return [r for r in rows
+            if r["Kernel_Name"].replace("void ", "", 1).startswith("(anonymous namespace)::")]
+
+
+def align_last_chunk(calls, dispatches):
+    """Match the last len(expanded calls) library dispatches to the calls:
+    returns [(call index, dispatch row)]; raises if a kernel family does not
+    match its call."""
+    fam = [(i, f) for i, c in enumerate(calls) for f in dispatch_families(c[0])]
+    if len(dispatches) < len(fam):
+        raise ValueError(f"{len(dispatches)} dispatches for {len(fam)} expected")
+    tail = dispatches[len(dispatches) - len(fam):]
+    out = []
+    for (i, f), r in zip(fam, tail):
+        k = short_kernel_name(r["Kernel_Name"])
+        if not k.startswith(f):
+            raise ValueError(f"call {i} ({calls[i][0]}) expects {f}, profiler shows {k}")
+        out.append((i, r))
+    return out
+
+
+def profile_table(calls, iso_us, trace_rows, pmc_rows, batch):
+    """Markdown of the in-chunk profile: per census group, the isolated replay
+    time, the in-chunk time (last replayed chunk of the kernel trace) and the
+    counter-derived figures (per dispatch, averaged over the group's launches
+    in the last eager chunk of each counter run)."""
+    import collections
+    al = align_last_chunk(calls, own_dispatches(trace_rows))
+    dur = collections.defaultdict(float)
+    kern = {}
+    for i, r in al:
+        dur[i] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        kern.setdefault(calls[i][4], short_kernel_name(r["Kernel_Name"]))
+    # counters: {call index: {counter: value}} from every counter run
+    cnt = collections.defaultdict(dict)
+    for rows in pmc_rows:
+        per = collections.OrderedDict()
+        for r in rows:
+            key = int(r["Dispatch_Id"])
+            d = per.setdefault(key, {"Kernel_Name": r["Kernel_Name"], "c": {}})
+            d["c"][r["Counter_Name"]] = d["c"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        disp = [{"Kernel_Name": v["Kernel_Name"], "c": v["c"]} for _, v in sorted(per.items())]
+        for i, d in align_last_chunk(calls, own_dispatches(disp)):
+            cnt[i].update(d["c"])
+    groups = collections.OrderedDict()
+    for i, (name, bound, fl, by, label) in enumerate(calls):
+        g = groups.setdefault(label, {"name": name, "bound": bound, "flops": fl, "bytes": by,
+                                      "idx": []})
+        g["idx"].append(i)
+    total = sum(dur.values())
+
+    def avg(g, key):
+        vals = [cnt[i][key] for i in g["idx"] if key in cnt[i]]
+        return sum(vals) / len(vals) if vals else None
+
+    rows = ["| # | group (entry point: shape, epilogue) | kernel | launches | isolated us | "
+            "in-chunk us | ms / chunk | % | in-chunk peak fraction | MFMA busy | issuing | "
+            "waiting | L2 hit | fetched / algorithmic |",
+            "|---:|---|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    order = sorted(groups.items(), key=lambda kv: -sum(dur[i] for i in kv[1]["idx"]))
+    ratio = lambda a, b, k=1.0: f"{k * a / b:.2f}" if a is not None and b else "-"  # noqa: E731
+    for n, (label, g) in enumerate(order[:30], 1):
+        t = sum(dur[i] for i in g["idx"])
+        us = t / len(g["idx"])
+        if g["bound"] == "mfma":
+            frac = g["flops"] / (us * 1e-6) / (PEAK_BF16_TFLOPS * 1e12)
+        else:
+            frac = g["bytes"] / (us * 1e-6) / (PEAK_HBM_GBS * 1e9)
+        wc = avg(g, "SQ_WAVE_CYCLES")
+        hit, miss = avg(g, "TCC_HIT"), avg(g, "TCC_MISS")
+        gui = avg(g, "GRBM_GUI_ACTIVE")
+        iso = iso_us.get(label)
+        rows.append(
+            f"| {n} | `{g['name']}`: {label} | `{kern.get(label, '?')[:56]}` | {len(g['idx'])} | "
+            f"{f'{iso:.2f}' if iso is not None else '-'} | {us:.2f} | {t / 1e3:.3f} | "
+            f"{100 * t / total:.1f} | {frac:.3f} ({'MFMA' if g['bound'] == 'mfma' else 'HBM'}) | "
+            f"{ratio(avg(g, 'SQ_VALU_MFMA_BUSY_CYCLES'), gui / N_XCD * N_SIMD if gui else None)} | "
+            f"{ratio(avg(g, 'SQ_ACTIVE_INST_ANY'), wc)} | {ratio(avg(g, 'SQ_WAIT_ANY'), wc)} | "
+            f"{ratio(hit, (hit + miss) if hit is not None and miss is not None else None)} | "
+            f"{ratio(avg(g, 'FETCH_SIZE'), g['bytes'], 1024 * FETCH_SCALE)} |")
+    return "\n".join(rows), total / 1e3, len(al)
