@@ -130,10 +130,10 @@ int svla_layernorm_blocked_bf16(const void* x, int ldx, const void* gamma, const
  * (cc/bf16_old/transpose_matmul_with_scale_bf16.cc:52, alpha = 0.125) and the
  * residual adds (vla/text_encoder_bf16.py:532,592).
  * norm_w (may be NULL): the A rows are RMS-normalised on the fly,
- *   C[m,n] = rsqrt(mean_k(x[m,:]^2) + norm_eps) * sum_k bf16(x[m,k] * norm_w[k]) * W[n,k]
- * (the scale applied to the fp32 product, before the epilogue: the same
- * normalised product as bf16(x * rsqrt(.) * w) . W up to one bf16 rounding);
- * K <= 2048.
+ *   C[m,n] = sum_k bf16((x[m,k] * r[m]) * norm_w[k]) * W[n,k],
+ *   r[m] = 1 / sqrt(mean_k(x[m,:]^2) + norm_eps)  (fp32),
+ * the operand rounded exactly as svla_rmsnorm_bf16 rounds its output, so the
+ * fused and the standalone norm give the same product; K <= 2048.
  * (the rmsnorm() that precedes every projection, vla/text_encoder_bf16.py:398-404).
  * Epilogue order (mirrors the torch modules' bf16 boundaries):
  *   v = alpha*acc (+ bias[n]) (+ bias_f32[n]); if out_f32: store fp32 v.

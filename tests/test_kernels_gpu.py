@@ -307,12 +307,12 @@ def test_fused_rmsnorm_prologue(ops, M, K):
     h = ref.rms_norm(x, nw, 1e-5)
     got = ops.linear(x.cuda(), wp, norm=(nw.cuda(), 1e-5))
     assert_close_bf16(got, ref.linear(h, w))
-    # vs the standalone RMSNorm kernel followed by the GEMM: the fused path
-    # rounds x * gain to bf16 and applies 1 / rms to the fp32 product, the
-    # standalone kernel rounds x * (1 / rms) * gain, so about half the operand
-    # elements differ in their last bit; after the SiLU-mul epilogue's bf16
-    # roundings of gate and up that is up to ~3 output ulps at the largest
-    # outputs: they agree to within 2^-6 of their range
+    # vs the standalone RMSNorm kernel followed by the GEMM: both round each
+    # operand element as bf16((x * (1 / rms)) * gain), so the operands are
+    # the same; the automatic tile choice can still differ (the 256-wide
+    # kernel takes no norm), and with it the fp32 summation order, so an
+    # output can move by an ulp or two (SiLU-mul rounds gate and up): within
+    # 2^-6 of the output range (bit-identical per forced tile below)
     def same(a, b):
         assert_close_bf16(a, b, rel=2 ** -6)
 
@@ -359,6 +359,45 @@ def test_every_tile_config_every_epilogue(ops, force_tile, tile):
     tails) through every epilogue, the fused RMSNorm and both A gathers."""
     force_tile(tile)
     _every_epilogue(ops, gen(100 + tile), tile)
+
+
+@pytest.mark.parametrize("tile", sorted(t for t in TILES if t != 8))
+def test_fused_norm_bit_identical_to_standalone(ops, force_tile, tile):
+    """Each kernel configuration that fuses the RMSNorm (all but the 256-wide
+    one) rounds every operand element as the standalone RMSNorm kernel rounds
+    its output, bf16((x * (1 / rms)) * gain): with the tile forced,
+    norm=(w, eps) on x and the same GEMM on svla_rmsnorm_bf16(x) are
+    bit-identical, through the plain, RoPE and SiLU-mul epilogues; ragged M,
+    a K tail, and K = 2048 (split over workgroups by the skinny tiles).  The
+    16- and 32-column skinny tiles are the exception: without the norm they
+    keep 8 k-steps per wave in flight, with it 4 (the gain fragments take
+    the registers), so their waves split K differently and the fp32 sums may
+    differ in order: there the outputs agree to an ulp or two."""
+    force_tile(tile)
+    g = gen(300 + tile)
+
+    def same(a, b, what):
+        if tile in (5, 12):
+            assert_close_bf16(a, b, rel=2 ** -6)
+        else:
+            assert torch.equal(a, b), what
+
+    for M, K in ((200, 200), (50, 720), (3, 2048)):
+        x = randn(g, M, K, std=2.0).cuda()
+        nw = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16).cuda()
+        nrm = (nw, 1e-5)
+        h = ops.rmsnorm(x, nw, 1e-5)
+        w = ops.pack_weight(randn(g, K, 192, std=0.05).cuda())
+        same(ops.linear(x, w, norm=nrm), ops.linear(h, w), ("plain", M, K))
+        if tile == 5:                                  # paired epilogues need 64-wide tiles
+            continue
+        c, s_ = ops.rope_table(M, 64, 1e4)
+        same(ops.linear_rope(x, w, 128, M, c, s_, norm=nrm),
+             ops.linear_rope(h, w, 128, M, c, s_), ("rope", M, K))
+        wgu = ops.pack_gate_up(randn(g, K, 128, std=0.05).cuda(),
+                               randn(g, K, 128, std=0.05).cuda())
+        same(ops.linear_silu_mul(x, wgu, norm=nrm), ops.linear_silu_mul(h, wgu),
+             ("silu", M, K))
 
 
 @pytest.mark.parametrize("tile,splits", [(4, 2), (5, 3), (4, 6), (5, 8), (12, 2), (12, 5)])

@@ -350,6 +350,82 @@ __device__ __forceinline__ void xcd_tile(const GemmArgs& p, int x, int i, int& t
   tn = (x / xg) * p.w_cn + i % p.w_cn;
 }
 
+// Fused RMSNorm (NORM), row scales: s_r[r] = 1 / rms of A row m0 + r, r < R,
+// computed before a kernel's main loop so that every operand element can then
+// be rounded once, bf16((x * r) * w[k]), exactly as the standalone RMSNorm
+// (rmsnorm_kernel) rounds its output; the accumulators need no row scale.
+// The sum of squares is formed in the standalone kernel's own order, so r and
+// with it every operand element are bit-identical to its: there one wave64
+// per row, lane l summing chunks l, l + 64, l + 128, l + 192 (8 bf16 each) by
+// fused multiply-adds, then a butterfly over xor 32, 16, 8, 4, 2, 1.  Here 8
+// threads per row: thread t plays lanes t + 8 i (i = 0..7), so the levels
+// xor 32, 16, 8 are local adds and xor 4, 2, 1 are shuffles.  One extra pass
+// over the tile's A rows: its first touch brings them into L2 for the main
+// loop; every 8 loads of a row are 128 contiguous bytes.  Rows past M are
+// clamped (their outputs are never stored).  K <= 2048.  The caller's barrier
+// publishes s_r.
+template <int R, int NT>
+__device__ __forceinline__ void norm_rows(const GemmArgs& p, int m0, float* s_r) {
+  constexpr int RPP = NT / 8;                // rows per pass
+  constexpr int NP = (R + RPP - 1) / RPP;    // passes: rows per thread
+  constexpr int PG = NP <= 3 ? NP : 2;       // passes whose loads are in flight together
+  static_assert(NP % PG == 0, "pass groups");
+  const int t = threadIdx.x & 7;
+  const int nj = (p.K + 511) / 512;
+#pragma unroll
+  for (int p0 = 0; p0 < NP; p0 += PG) {
+    const bf16* x[PG];
+    float v[PG][8];  // pass p0 + pp, lane t + 8 i's sum
+#pragma unroll
+    for (int pp = 0; pp < PG; ++pp) {
+      x[pp] = p.a + (long)min(m0 + (p0 + pp) * RPP + (int)(threadIdx.x >> 3), p.M - 1) * p.lda;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[pp][i] = 0.f;
+    }
+    // every load of a round is issued unconditionally from a clamped address
+    // (a load under a branch ends its region with a full vmcnt drain) and a
+    // chunk past K contributes fma(0, 0, v) = v, as the standalone kernel's
+    // skipped chunk does
+    for (int j = 0; j < nj; ++j) {
+      bf16x8 q[PG][8];
+#pragma unroll
+      for (int pp = 0; pp < PG; ++pp)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          q[pp][i] = ld8(x[pp] + min((t + 8 * i + 64 * j) * 8, p.K - 8));
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const bool in = (t + 8 * i + 64 * j) * 8 < p.K;
+#pragma unroll
+        for (int pp = 0; pp < PG; ++pp)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float f = in ? bf2f(q[pp][i][e]) : 0.f;
+            v[pp][i] = __builtin_fmaf(f, f, v[pp][i]);
+          }
+      }
+    }
+#pragma unroll
+    for (int pp = 0; pp < PG; ++pp) {
+      // lane bits 5, 4, 3 are i's bits 2, 1, 0
+      const float u0 = (v[pp][0] + v[pp][4]) + (v[pp][2] + v[pp][6]);
+      const float u1 = (v[pp][1] + v[pp][5]) + (v[pp][3] + v[pp][7]);
+      float s = u0 + u1;
+      s += __shfl_xor(s, 4, 64);
+      s += __shfl_xor(s, 2, 64);
+      s += __shfl_xor(s, 1, 64);
+      const int r = (p0 + pp) * RPP + (int)(threadIdx.x >> 3);
+      if (t == 0 && (R % RPP == 0 || r < R)) s_r[r] = 1.0f / sqrtf(s / (float)p.K + p.norm_eps);
+    }
+  }
+}
+
+// bf16((x * r) * w): one operand fragment of a normalised row (scale r, gain w)
+__device__ __forceinline__ void norm_frag(bf16x8& x, float r, const bf16x8& w) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = f2bf(__fmul_rn(__fmul_rn(bf2f(x[j]), r), bf2f(w[j])));
+}
+
 template <int BM, int BN, int WAVES_M, int WAVES_N, int MF, int AMODE, bool NORM, int EPI,
           int ACT>
 __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs p) {
@@ -386,13 +462,12 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
   const int kt_begin = 0;
   const int kt_end = (p.K + BK - 1) / BK;
 
-  // Fused RMSNorm (NORM): the A chunks are multiplied by the gain on their
-  // way into LDS while their squares are summed (each row's K is spread over
-  // the 8 consecutive threads that own its chunks); the row scale 1 / rms
-  // multiplies the accumulators in the epilogue.  No pass over A of its own.
-  float ssq[NORM ? A_CH : 1];
-#pragma unroll
-  for (int i = 0; i < (NORM ? A_CH : 1); ++i) ssq[i] = 0.f;
+  // Fused RMSNorm (NORM): row scales first (norm_rows), then each A chunk is
+  // rounded as bf16((x * r) * w) on its way into LDS.
+  if constexpr (NORM) {
+    norm_rows<BM, 256>(p, m0, s_rs);
+    __syncthreads();
+  }
 
   acc_t acc[TN][TM];
 #pragma unroll
@@ -432,14 +507,7 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
     for (int i = 0; i < A_CH; ++i) {
       const int c = tid + i * 256;
       bf16x8 v = kin ? ra[i] : bf16x8{};
-      if constexpr (NORM) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float xv = bf2f(v[j]);
-          ssq[i] = __builtin_fmaf(xv, xv, ssq[i]);
-          v[j] = f2bf(__fmul_rn(xv, bf2f(rw[j])));
-        }
-      }
+      if constexpr (NORM) norm_frag(v, s_rs[c >> 3], rw);
       *reinterpret_cast<bf16x8*>(&sA[buf][(c >> 3) * LDS_STRIDE + (c & 7) * 8]) = v;
     }
 #pragma unroll
@@ -487,17 +555,6 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
       __syncthreads();
     }
   }
-  if constexpr (NORM) {
-#pragma unroll
-    for (int i = 0; i < A_CH; ++i) {
-      float t = ssq[i];
-      t += __shfl_xor(t, 1, 64);
-      t += __shfl_xor(t, 2, 64);
-      t += __shfl_xor(t, 4, 64);
-      if ((tid & 7) == 0) s_rs[(tid + i * 256) >> 3] = 1.0f / sqrtf(t / (float)p.K + p.norm_eps);
-    }
-    __syncthreads();
-  }
 
   // ---- accumulator layout: acc[tn][tm][r] = C[m][n] with
   //   m = m0 + wm*WM + tm*MF + lane % MF
@@ -533,11 +590,10 @@ __global__ __launch_bounds__(256, (BM >= 256 ? 1 : 2)) void gemm_kernel(GemmArgs
         const int n = n0 + wn * WN + tn * MF + q * RUN_STRIDE + col_in;
         if (m >= p.M || n >= p.N) continue;
         float x1[4], x2[4];
-        const float sc = NORM ? p.alpha * s_rs[wm * WM + tm * MF + (lane % MF)] : p.alpha;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          x1[i] = acc[tn][tm][4 * q + i] * sc;
-          x2[i] = PAIRED ? acc[(tn + PAIR_T) % TN][tm][4 * q + i] * sc : 0.f;
+          x1[i] = acc[tn][tm][4 * q + i] * p.alpha;
+          x2[i] = PAIRED ? acc[(tn + PAIR_T) % TN][tm][4 * q + i] * p.alpha : 0.f;
         }
         epi_apply<EPI, ACT>(p, m, n, x1, x2, e[tm * RUNS + q]);
       }
@@ -564,12 +620,10 @@ constexpr int PBK = 32;
 __device__ __forceinline__ int pswz(int r, int g) { return g ^ ((r >> 1) & 3); }
 
 // Epilogue of the LDS-DMA pipelines (same lane layout as gemm_kernel with
-// MF = 16), one column tile at a time: all loads, then all stores.  rs: the
-// row scale 1 / rms of the lane's rows (NORM).
-template <int BM, int BN, int EPI, int ACT, bool NORM, int TN, int TM>
+// MF = 16), one column tile at a time: all loads, then all stores.
+template <int BM, int BN, int EPI, int ACT, int TN, int TM>
 __device__ __forceinline__ void pipe_epilogue(const GemmArgs& p, const f32x4 (&acc)[TN][TM],
-                                              const float (&rs)[TM], int m0, int n0, int wm,
-                                              int wn, int fr, int g) {
+                                              int m0, int n0, int wm, int wn, int fr, int g) {
   constexpr int WAVES_M = BM >= 128 ? 2 : 4, WAVES_N = 4 / WAVES_M;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr bool PAIRED = EPI == EPI_ROPE || EPI == EPI_SILU;
@@ -593,11 +647,10 @@ __device__ __forceinline__ void pipe_epilogue(const GemmArgs& p, const f32x4 (&a
       const int m = m0 + wm * WM + tm * 16 + fr;
       if (m >= p.M || n >= p.N) continue;
       float x1[4], x2[4];
-      const float sc = NORM ? p.alpha * rs[tm] : p.alpha;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        x1[i] = acc[tn][tm][i] * sc;
-        x2[i] = PAIRED ? acc[(tn + 2) % TN][tm][i] * sc : 0.f;
+        x1[i] = acc[tn][tm][i] * p.alpha;
+        x2[i] = PAIRED ? acc[(tn + 2) % TN][tm][i] * p.alpha : 0.f;
       }
       epi_apply<EPI, ACT>(p, m, n, x1, x2, e[tm]);
     }
@@ -618,6 +671,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) bf16 sB0[BN * PBK], sB1[BN * PBK],
       sB2[BN * PBK], sB3[BN * PBK];
   __shared__ __attribute__((aligned(16))) bf16 s_gain[NORM ? 2048 : 8];  // norm gain (K <= 2048)
+  __shared__ float s_r[NORM ? BM : 1];                                    // norm row scales
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -628,13 +682,6 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
   const int m0 = tm_idx * BM, n0 = tn_idx * BN;
   const int nk = p.K / PBK;  // full K steps (>= 1, checked by the launcher)
 
-  if constexpr (NORM) {
-    // the gain vector lives in LDS so the main loop issues no global loads
-    // besides its DMA (a plain load would force a full vmcnt drain)
-    for (int c = tid * 8; c < p.K; c += 256 * 8)
-      *reinterpret_cast<bf16x8*>(&s_gain[c]) = ld8(p.norm_w + c);
-    __syncthreads();
-  }
 
   // per-lane DMA source rows (fixed across K tiles): block b covers rows
   // 16b .. 16b+15, lane -> row 16b + lane/4, slot lane%4
@@ -695,26 +742,28 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
     for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int fr = lane & 15, g = lane >> 4;
-  // Fused RMSNorm (NORM): every wave reads the A fragments of its rows over
-  // the whole K, so it multiplies them by the gain and sums their squares on
-  // the way into the MFMAs (lane: row tm * 16 + fr, columns g * 8 .. + 7 of
-  // each K step); the row scale 1 / rms multiplies the accumulators in the
-  // epilogue.  No pass over A of its own.
-  float ssq[TM];
+  // Fused RMSNorm (NORM): the gain vector is copied to LDS (the main loop
+  // then issues no global loads besides its DMA: a plain load would force a
+  // full vmcnt drain) and the row scales are formed (norm_rows) while the
+  // first stages stream in; each A fragment (lane: row tm * 16 + fr, columns
+  // g * 8 .. + 7 of a K step) is rounded as bf16((x * r) * w) on its way into
+  // the MFMAs.
+  float rsv[TM];  // row scale of the lane's fragment row in row tile tm
+  auto norm_setup = [&]() __attribute__((always_inline)) {
+    if constexpr (NORM) {
+      for (int c = tid * 8; c < p.K; c += 256 * 8)
+        *reinterpret_cast<bf16x8*>(&s_gain[c]) = ld8(p.norm_w + c);
+      norm_rows<BM, 256>(p, m0, s_r);
+      __syncthreads();
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) ssq[tm] = 0.f;
-
+      for (int tm = 0; tm < TM; ++tm) rsv[tm] = s_r[wm * WM + tm * 16 + fr];
+    }
+  };
   auto normalise = [&](bf16x8 (&fx)[TM], int k) {
     if constexpr (NORM) {
       const bf16x8 gw = *reinterpret_cast<const bf16x8*>(&s_gain[k]);
 #pragma unroll
-      for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float xv = bf2f(fx[tm][j]);
-          ssq[tm] = __builtin_fmaf(xv, xv, ssq[tm]);
-          fx[tm][j] = f2bf(__fmul_rn(xv, bf2f(gw[j])));
-        }
+      for (int tm = 0; tm < TM; ++tm) norm_frag(fx[tm], rsv[tm], gw);
     }
   };
   auto mma = [&](const bf16x8 (&fw)[TN], const bf16x8 (&fx)[TM]) {
@@ -772,6 +821,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
   issue(I0{}, 0);
   issue(I1{}, 1);
   issue(I2{}, 2);
+  norm_setup();
   for (int kt = 0; kt < nk; kt += 4) {
     sync_step();
     issue(I3{}, kt + 3);
@@ -803,17 +853,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pipe_kernel(GemmArgs p) {
     normalise(fx, min(k, p.K - 8));  // fx is zero past K whatever the gain
     mma(fw, fx);
   }
-  float rs[TM];  // row scale of row tm * 16 + fr (the lane's epilogue rows)
-  if constexpr (NORM) {
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-      float t = ssq[tm];
-      t = xor32_sum(xor16_sum(t));
-      rs[tm] = 1.0f / sqrtf(t / (float)p.K + p.norm_eps);
-    }
-  }
-
-  pipe_epilogue<BM, BN, EPI, ACT, NORM>(p, acc, rs, m0, n0, wm, wn, fr, g);
+  pipe_epilogue<BM, BN, EPI, ACT>(p, acc, m0, n0, wm, wn, fr, g);
 }
 
 // ---- line-DMA pipeline: 64-wide K stages fetched as whole cache lines ------
@@ -842,6 +882,7 @@ __global__ __launch_bounds__(256, 2) void gemm_line_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(1024))) bf16 sA0[BM * LBK], sA1[BM * LBK];
   __shared__ __attribute__((aligned(1024))) bf16 sB0[BN * LBK], sB1[BN * LBK];
   __shared__ __attribute__((aligned(16))) bf16 s_gain[NORM ? 2048 : 8];  // norm gain (K <= 2048)
+  __shared__ float s_r[NORM ? BM : 1];                                    // norm row scales
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
@@ -851,12 +892,6 @@ __global__ __launch_bounds__(256, 2) void gemm_line_kernel(GemmArgs p) {
   tile_coords(tile, gridDim.y, gn, tm_idx, tn_idx);
   const int m0 = tm_idx * BM, n0 = tn_idx * BN;
   const int nk = p.K / LBK;  // full 64-wide stages (>= 1, checked by the launcher)
-
-  if constexpr (NORM) {
-    for (int c = tid * 8; c < p.K; c += 256 * 8)
-      *reinterpret_cast<bf16x8*>(&s_gain[c]) = ld8(p.norm_w + c);
-    __syncthreads();
-  }
 
   // per-lane DMA source rows (fixed across stages): block b covers rows
   // 8b .. 8b+7, lane -> row 8b + lane/8, LDS slot lane%8
@@ -917,22 +952,24 @@ __global__ __launch_bounds__(256, 2) void gemm_line_kernel(GemmArgs p) {
     for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int fr = lane & 15, g = lane >> 4;
-  // fused RMSNorm as in gemm_pipe_kernel: gain on the way in, row sums of
-  // squares from the same fragments, 1 / rms in the epilogue
-  float ssq[TM];
+  // fused RMSNorm as in gemm_pipe_kernel: gain to LDS and row scales while
+  // the first stage streams in, bf16((x * r) * w) on the way into the MFMAs
+  float rsv[TM];
+  auto norm_setup = [&]() __attribute__((always_inline)) {
+    if constexpr (NORM) {
+      for (int c = tid * 8; c < p.K; c += 256 * 8)
+        *reinterpret_cast<bf16x8*>(&s_gain[c]) = ld8(p.norm_w + c);
+      norm_rows<BM, 256>(p, m0, s_r);
+      __syncthreads();
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) ssq[tm] = 0.f;
+      for (int tm = 0; tm < TM; ++tm) rsv[tm] = s_r[wm * WM + tm * 16 + fr];
+    }
+  };
   auto normalise = [&](bf16x8 (&fx)[TM], int k) {
     if constexpr (NORM) {
       const bf16x8 gw = *reinterpret_cast<const bf16x8*>(&s_gain[k]);
 #pragma unroll
-      for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float xv = bf2f(fx[tm][j]);
-          ssq[tm] = __builtin_fmaf(xv, xv, ssq[tm]);
-          fx[tm][j] = f2bf(__fmul_rn(xv, bf2f(gw[j])));
-        }
+      for (int tm = 0; tm < TM; ++tm) norm_frag(fx[tm], rsv[tm], gw);
     }
   };
   auto mma = [&](const bf16x8 (&fw)[TN], const bf16x8 (&fx)[TM]) {
@@ -981,6 +1018,7 @@ __global__ __launch_bounds__(256, 2) void gemm_line_kernel(GemmArgs p) {
   using I1 = std::integral_constant<int, 1>;
 
   issue(I0{}, 0);
+  norm_setup();
   for (int kt = 0; kt < nk; kt += 2) {
     sync_step();
     issue(I1{}, kt + 1);
@@ -1006,16 +1044,7 @@ __global__ __launch_bounds__(256, 2) void gemm_line_kernel(GemmArgs p) {
     normalise(fx, min(k, p.K - 8));  // fx is zero past K whatever the gain
     mma(fw, fx);
   }
-  float rs[TM];  // row scale of row tm * 16 + fr (the lane's epilogue rows)
-  if constexpr (NORM) {
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-      float t = ssq[tm];
-      t = xor32_sum(xor16_sum(t));
-      rs[tm] = 1.0f / sqrtf(t / (float)p.K + p.norm_eps);
-    }
-  }
-  pipe_epilogue<BM, BN, EPI, ACT, NORM>(p, acc, rs, m0, n0, wm, wn, fr, g);
+  pipe_epilogue<BM, BN, EPI, ACT>(p, acc, m0, n0, wm, wn, fr, g);
 }
 
 // ---- small-tile GEMM: BM x BN block tile, 4-stage line-DMA ring -------------
@@ -1032,9 +1061,8 @@ __global__ __launch_bounds__(256, 2) void gemm_line_kernel(GemmArgs p) {
 // and each weight fragment twice (once per row half).  The two K halves meet
 // in LDS at the end; waves 0 and 1 run the epilogue (the same
 // lane layout as the pipelines: 4 consecutive columns of one row per lane).
-// The fused RMSNorm works as in the line kernel (gain on the way into the
-// MFMAs, row sums of squares from the same fragments, 1 / rms in the
-// epilogue), its two K halves summed with the tiles.
+// The fused RMSNorm works as in the line kernel (row scales first, each A
+// fragment rounded as bf16((x * r) * w) on the way into the MFMAs).
 constexpr int SNS = 4;  // ring stages
 
 template <int BM, int BN, int AMODE, bool NORM, int EPI, int ACT>
@@ -1051,8 +1079,8 @@ __global__ __launch_bounds__(256, (BM * BN <= 2048 ? 2 : 1)) void gemm_small_ker
   __shared__ __attribute__((aligned(1024))) bf16 sB0[BN * LBK], sB1[BN * LBK],
       sB2[BN * LBK], sB3[BN * LBK];
   __shared__ __attribute__((aligned(16))) bf16 s_gain[NORM ? 2048 : 8];  // K <= 2048
+  __shared__ float s_r[NORM ? BM : 1];                                      // norm row scales
   __shared__ __attribute__((aligned(16))) float s_red[2][TM * TN * 4][64];  // K-half 1's tiles
-  __shared__ float s_ss[2][TM][64];                                         // ... and row sums
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, kg = wave >> 1;
@@ -1062,12 +1090,6 @@ __global__ __launch_bounds__(256, (BM * BN <= 2048 ? 2 : 1)) void gemm_small_ker
   tile_coords(tile, gridDim.y, gn, tm_idx, tn_idx);
   const int m0 = tm_idx * BM, n0 = tn_idx * BN;
   const int nk = p.K / LBK;  // full 64-wide stages (>= 1, checked by the launcher)
-
-  if constexpr (NORM) {
-    for (int c = tid * 8; c < p.K; c += 256 * 8)
-      *reinterpret_cast<bf16x8*>(&s_gain[c]) = ld8(p.norm_w + c);
-    __syncthreads();
-  }
 
   // DMA rows: block b covers rows 8b .. 8b + 7, wave w issues blocks
   // w * X_DMA + j; lane -> row lane / 8, chunk lane % 8 at slot lswz(row, chunk)
@@ -1108,20 +1130,24 @@ __global__ __launch_bounds__(256, (BM * BN <= 2048 ? 2 : 1)) void gemm_small_ker
     for (int j = 0; j < TM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
   const int fr = lane & 15, g = lane >> 4;
   const int arow0 = wm * (BM / 2) + fr;  // the lane's A fragment row in row tile 0
-  float ssq[TM];
+  // fused RMSNorm as in gemm_pipe_kernel: gain to LDS and row scales while
+  // the first stages stream in, bf16((x * r) * w) on the way into the MFMAs
+  float rsv[TM];
+  auto norm_setup = [&]() __attribute__((always_inline)) {
+    if constexpr (NORM) {
+      for (int c = tid * 8; c < p.K; c += 256 * 8)
+        *reinterpret_cast<bf16x8*>(&s_gain[c]) = ld8(p.norm_w + c);
+      norm_rows<BM, 256>(p, m0, s_r);
+      __syncthreads();
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) ssq[tm] = 0.f;
+      for (int tm = 0; tm < TM; ++tm) rsv[tm] = s_r[arow0 + tm * 16];
+    }
+  };
   auto step = [&](const bf16x8 (&fw)[TN], bf16x8 (&fx)[TM], int k) __attribute__((always_inline)) {
     if constexpr (NORM) {
       const bf16x8 gw = *reinterpret_cast<const bf16x8*>(&s_gain[k]);
 #pragma unroll
-      for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float xv = bf2f(fx[tm][j]);
-          ssq[tm] = __builtin_fmaf(xv, xv, ssq[tm]);
-          fx[tm][j] = f2bf(__fmul_rn(xv, bf2f(gw[j])));
-        }
+      for (int tm = 0; tm < TM; ++tm) norm_frag(fx[tm], rsv[tm], gw);
     }
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
@@ -1169,6 +1195,7 @@ __global__ __launch_bounds__(256, (BM * BN <= 2048 ? 2 : 1)) void gemm_small_ker
   issue(I0{}, 0);
   issue(I1{}, 1);
   issue(I2{}, 2);
+  norm_setup();
   for (int kt = 0; kt < nk; kt += SNS) {
     sync_step();
     issue(I3{}, kt + 3);
@@ -1201,11 +1228,7 @@ __global__ __launch_bounds__(256, (BM * BN <= 2048 ? 2 : 1)) void gemm_small_ker
     step(fw, fx, min(k, p.K - 8));  // fx is zero past K whatever the gain
   }
 
-  // the two K halves meet: waves 2, 3 hand their tiles (and row sums) to 0, 1
-  if constexpr (NORM) {
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) ssq[tm] = xor32_sum(xor16_sum(ssq[tm]));
-  }
+  // the two K halves meet: waves 2, 3 hand their tiles to 0, 1
   if (kg == 1) {
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
@@ -1213,10 +1236,6 @@ __global__ __launch_bounds__(256, (BM * BN <= 2048 ? 2 : 1)) void gemm_small_ker
       for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
         for (int i = 0; i < 4; ++i) s_red[wm][(tn * TM + tm) * 4 + i][lane] = acc[tn][tm][i];
-    if constexpr (NORM) {
-#pragma unroll
-      for (int tm = 0; tm < TM; ++tm) s_ss[wm][tm][lane] = ssq[tm];
-    }
   }
   __syncthreads();
   if (kg == 1) return;
@@ -1226,10 +1245,6 @@ __global__ __launch_bounds__(256, (BM * BN <= 2048 ? 2 : 1)) void gemm_small_ker
     for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[tn][tm][i] += s_red[wm][(tn * TM + tm) * 4 + i][lane];
-  float rs[TM];
-#pragma unroll
-  for (int tm = 0; tm < TM; ++tm)
-    rs[tm] = NORM ? 1.0f / sqrtf((ssq[tm] + s_ss[wm][tm][lane]) / (float)p.K + p.norm_eps) : 1.f;
 
   // epilogue: lane holds columns n0 + 16 tn + 4 g .. + 3 of rows m0 + arow0 +
   // 16 tm; paired epilogues (RoPE / SiLU) combine tile tn < 2 with tile tn + 2
@@ -1238,7 +1253,7 @@ __global__ __launch_bounds__(256, (BM * BN <= 2048 ? 2 : 1)) void gemm_small_ker
 #pragma unroll
   for (int tm = 0; tm < TM; ++tm) {
     const int m = m0 + arow0 + tm * 16;
-    const float sc = NORM ? p.alpha * rs[tm] : p.alpha;
+    const float sc = p.alpha;
     int gm[G], gnn[G];
     EpiIn e[G];
 #pragma unroll
@@ -1732,17 +1747,14 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmArgs p) {
 // (in steps of 32) and each accumulates the whole tile with 16x16x32 MFMAs
 // whose operand fragments come straight from global memory.  Problems this
 // small are latency-bound, so each wave issues the loads of up to KR k-steps
-// at once before any MFMA.  The optional RMSNorm of the A rows needs no pass
-// of its own: each wave multiplies its A fragments by the gain only and sums
-// their squares on the way into the MFMAs, so a row's statistics are complete
-// once the partial tiles meet, and the row scale 1 / rms multiplies the summed
-// tile in the epilogue.  The 8 partial tiles (and row sums of squares) are
-// summed through LDS and all 512 threads run the epilogue.
+// at once before any MFMA.  The optional RMSNorm of the A rows forms the row
+// scales first (norm_rows, over the whole K whatever the split) and rounds
+// each A fragment as bf16((x * r) * w) on its way into the MFMAs.  The 8
+// partial tiles are summed through LDS and all 512 threads run the epilogue.
 //
 // Split-K over workgroups (gridDim.z = S > 1, for long-K problems whose grid
 // is far smaller than the chip): workgroup z covers k-steps
-// [z * kps, (z + 1) * kps) and writes its fp32 tile (and, with the norm, its
-// BM partial row sums of squares) to the workspace; the last of the S
+// [z * kps, (z + 1) * kps) and writes its fp32 tile to the workspace; the last of the S
 // workgroups of a tile to arrive (device-scope counter) sums the S partials in
 // split order, runs the epilogue and resets the counter.  No workgroup ever
 // waits for another.
@@ -1756,8 +1768,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
   // k-steps whose loads are in flight together (bounded by the 256-VGPR budget
   // of 8 waves per workgroup); 8 waves x 4 steps cover K <= 1024 in one round
   constexpr int KR = BN <= 32 && AMODE == A_DENSE && !NORM ? 8 : 4;
-  // one split's workspace partial: the tile, then (norm) its row sums of squares
-  constexpr int PSZ = BM * BN + (NORM ? BM : 0);
+  constexpr int PSZ = BM * BN;  // one split's workspace partial
   // Paired epilogues (RoPE / SiLU) combine packed column n with n + 32 of the
   // same 64-column block.  A 64-wide tile holds both halves; a 16-wide tile
   // (P16) takes 8 columns of a first half and their 8 partners, loading the
@@ -1769,8 +1780,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
   static_assert(!PAIRED || BN % 64 == 0 || P16, "paired epilogue");
   static_assert(!NORM || AMODE == A_DENSE, "row norm only for dense A");
   __shared__ __attribute__((aligned(16))) float s_part[SK_WAVES][BM * PS];
-  __shared__ float s_ss[NORM ? SK_WAVES : 1][BM];  // per-wave row sums of squares
-  __shared__ float s_rs[NORM ? BM : 1];            // row scale 1 / rms
+  __shared__ float s_rs[NORM ? BM : 1];            // norm row scales
   __shared__ int s_last;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -1818,19 +1828,17 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
 #pragma unroll
     for (int r = 0; r < KR; ++r) load_step(r, min(base + r, ks1 - 1) * 32 + fk);
   };
-  float ss[TM];  // norm: this lane's sum of squares of row tm * 16 + fr
+  float rsv[TM];  // norm: row scale of row tm * 16 + fr
+  if constexpr (NORM) {
+    norm_rows<BM, NT>(p, m0, s_rs);
+    __syncthreads();
 #pragma unroll
-  for (int tm = 0; tm < TM; ++tm) ss[tm] = 0.f;
+    for (int tm = 0; tm < TM; ++tm) rsv[tm] = s_rs[tm * 16 + fr];
+  }
   auto mma_step = [&](int r) __attribute__((always_inline)) {
     if constexpr (NORM) {
 #pragma unroll
-      for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float xv = bf2f(fx[r][tm][j]);
-          ss[tm] = __builtin_fmaf(xv, xv, ss[tm]);
-          fx[r][tm][j] = f2bf(__fmul_rn(xv, bf2f(fg[r][j])));
-        }
+      for (int tm = 0; tm < TM; ++tm) norm_frag(fx[r][tm], rsv[tm], fg[r]);
     }
 #pragma unroll
     for (int tn = 0; tn < TN; ++tn)
@@ -1875,24 +1883,7 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
     for (int tn = 0; tn < TN; ++tn)
       *reinterpret_cast<f32x4*>(&s_part[wave][(tm * 16 + fr) * PS + tn * 16 + 4 * (lane >> 4)]) =
           acc[tn][tm];
-  if constexpr (NORM) {
-#pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-      float t = ss[tm];
-      t = xor32_sum(xor16_sum(t));
-      if (lane < 16) s_ss[wave][tm * 16 + lane] = t;
-    }
-  }
   __syncthreads();
-  auto wave_ss = [&](int ml) __attribute__((always_inline)) {
-    float t = s_ss[0][ml];
-#pragma unroll
-    for (int w = 1; w < SK_WAVES; ++w) t += s_ss[w][ml];
-    return t;
-  };
-  auto set_rs = [&](int ml, float sumsq) __attribute__((always_inline)) {
-    s_rs[ml] = 1.0f / sqrtf(sumsq / (float)p.K + p.norm_eps);
-  };
 
   auto wave_sum4 = [&](int ml, int nl) __attribute__((always_inline)) {
     f32x4 t = *reinterpret_cast<const f32x4*>(&s_part[0][ml * PS + nl]);
@@ -1921,11 +1912,6 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
       for (int i = 0; i < 4; ++i)
         __hip_atomic_store(d + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if constexpr (NORM) {
-      if (tid < BM)
-        __hip_atomic_store(wt + (long)z * PSZ + BM * BN + tid, wave_ss(tid), __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
-    }
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     __builtin_amdgcn_s_waitcnt(waitcnt_imm(0, 15));
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -1948,28 +1934,15 @@ __global__ __launch_bounds__(SK_WAVES * 64) void skinny_kernel(GemmArgs p) {
       }
       *reinterpret_cast<f32x4*>(&s_part[0][ml * PS + nl]) = t;
     }
-    if constexpr (NORM) {
-      if (tid < BM) {
-        float t = 0.f;
-        for (int zz = 0; zz < S; ++zz)
-          t += __hip_atomic_load(wt + (long)zz * PSZ + BM * BN + tid, __ATOMIC_RELAXED,
-                                 __HIP_MEMORY_SCOPE_AGENT);
-        set_rs(tid, t);
-      }
-    }
     if (tid == 0)  // ready for the next call
       __hip_atomic_store(p.ws_cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-  } else if constexpr (NORM) {
-    if (tid < BM) set_rs(tid, wave_ss(tid));
     __syncthreads();
   }
   auto sum4 = [&](int ml, int nl, float v[4]) __attribute__((always_inline)) {
     const f32x4 t = S > 1 ? *reinterpret_cast<const f32x4*>(&s_part[0][ml * PS + nl])
                           : wave_sum4(ml, nl);
-    const float sc = NORM ? p.alpha * s_rs[ml] : p.alpha;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = t[i] * sc;
+    for (int i = 0; i < 4; ++i) v[i] = t[i] * p.alpha;
   };
   // every thread handles ITER output groups: all their loads, then all stores
   // units per row: 4-column groups (paired: of the first half of each 64-block,
@@ -2435,8 +2408,8 @@ int pick_split(int tiles, int K, int bm, int bn) {
   }
   S = min(S, max(1, nkf));
   // workspace capacity
-  // (a partial is the fp32 tile plus bm row sums of squares for a fused norm)
-  while (S > 1 && ((size_t)tiles * S * (bm * bn + bm) > kWsFloats || tiles > kWsTiles)) --S;
+  // (a partial is the fp32 tile)
+  while (S > 1 && ((size_t)tiles * S * bm * bn > kWsFloats || tiles > kWsTiles)) --S;
   return max(S, 1);
 }
 
@@ -2483,7 +2456,7 @@ int run_gemm(GemmArgs& p, int epi, int act, hipStream_t s, WsKind wk = WS_ALLOCA
   const bool wide_rows_ok = !p.out_f32 && p.N % 8 == 0 && p.ldc % 8 == 0 &&
                             (!p.res || (p.ldr % 8 == 0 && svla_aligned16(p.res)));
   const TileCfg t = pick_tile(p.M, p.N, p.K, epi, plain, wide_rows_ok, AMODE == A_DENSE);
-  if (p.norm_w && p.K > 2048) return SVLA_EINVAL;  // row statistics keep <= 2048 per row
+  if (p.norm_w && p.K > 2048) return SVLA_EINVAL;  // the gain vector is staged in LDS (<= 2048)
   // a pipelined kernel needs one full K stage, the wide one whole 4-step
   // rounds of at least 8 steps (a strictly forced tile may violate either:
   // refused here, before any launch)

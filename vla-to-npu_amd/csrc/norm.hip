@@ -13,6 +13,8 @@ namespace {
 
 constexpr int MAXC = 4;  // 16-byte chunks per lane: cols <= 4 * 8 * 64 = 2048
 
+// (The GEMMs' fused norm, norm_rows in gemm.hip, reproduces this kernel's
+// sum of squares operation by operation: change both together.)
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16* __restrict__ x, long ldx,
                                                       const bf16* __restrict__ w,
                                                       bf16* __restrict__ y, long ldy, int rows,
@@ -31,7 +33,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16* __restrict__ x
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float f = bf2f(v[i][j]);
-        ss += f * f;
+        ss = __builtin_fmaf(f, f, ss);
       }
     }
   }

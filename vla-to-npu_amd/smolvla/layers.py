@@ -8,15 +8,16 @@ captured in one HIP graph.  Activations are row-major ``[B*S, H]`` bf16.
 Per decoder layer (vla/text_encoder_bf16.py:480-595 -> 7 launches):
   RMSNorm -> [QKV GEMM -> RoPE] -> fused GQA attention -> [O GEMM + residual]
   -> RMSNorm -> [gate|up GEMM -> SiLU*up] -> [down GEMM + residual]
-(brackets = one kernel).  The RMSNorm runs as its own bandwidth kernel, which
-rounds once, bf16(x * (1/rms) * gain), as torch's bf16 RMSNorm does; the
-GEMMs can also fuse the norm into their A path (``norm=``), but then round
-bf16(x * gain) and scale by 1/rms in the epilogue, a different rounding point
-that moves a layer output by up to ~1e-2 relative on real activations, so the
-layers here do not use it (measured on MI355X it saved at most ~1.3 us per
-norm: expert at batch 32, M = 1600, gate|up 22.9 us fused vs 24.2 us).  RoPE'd
-Q and K also carry their bf16 remainders into the attention, which then scores
-the fp32 values as the reference module does.
+(brackets = one kernel).  Each RMSNorm rounds once, bf16((x * (1/rms)) *
+gain), as torch's bf16 RMSNorm does.  It runs as its own bandwidth kernel
+into a buffer.  The GEMMs can also take it in their A path (``norm=``: each
+workgroup forms its rows' 1/rms first, then rounds every operand element the
+same way, bit-identical operands), but that extra pass over a tile's A rows
+costs more than the standalone kernel on every engine shape measured on
+MI355X (batch-32 chunk 41.3 ms with standalone norms, 42.4 ms fused; batch-1
+chunk 8.13 vs 8.15 ms), so FUSED_NORM_MAX_ROWS keeps it off.  RoPE'd Q and K
+also carry their bf16 remainders into the attention, which then scores the
+fp32 values as the reference module does.
 """
 
 from __future__ import annotations
@@ -174,8 +175,8 @@ class Buffers:
 
 
 # ----------------------------------------------------------------- layers ---
-# fuse the RMSNorm into the consuming GEMM up to this many rows; 0: never
-# (the standalone kernel keeps the reference's single rounding, see above)
+# fuse the RMSNorm into the consuming GEMM up to this many rows (the same
+# rounding either way; 0: never, the faster choice measured, see above)
 FUSED_NORM_MAX_ROWS = 0
 
 
