@@ -347,10 +347,14 @@ def profile_table(calls, iso_us, trace_rows, pmc_rows, batch):
     import collections
     al = align_last_chunk(calls, own_dispatches(trace_rows))
     dur = collections.defaultdict(float)
-    kern = {}
+    kern, kern_us = {}, {}
     for i, r in al:
-        dur[i] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
-        kern.setdefault(calls[i][4], short_kernel_name(r["Kernel_Name"]))
+        us = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        dur[i] += us
+        # a call with several dispatches (the fused expert's clear + launch)
+        # is labelled by its longest one
+        if us > kern_us.get(calls[i][4], -1.0):
+            kern[calls[i][4]], kern_us[calls[i][4]] = short_kernel_name(r["Kernel_Name"]), us
     # counters: {call index: {counter: value}} from every counter run
     cnt = collections.defaultdict(dict)
     for rows in pmc_rows:
@@ -361,7 +365,8 @@ def profile_table(calls, iso_us, trace_rows, pmc_rows, batch):
             d["c"][r["Counter_Name"]] = d["c"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
         disp = [{"Kernel_Name": v["Kernel_Name"], "c": v["c"]} for _, v in sorted(per.items())]
         for i, d in align_last_chunk(calls, own_dispatches(disp)):
-            cnt[i].update(d["c"])
+            for k, v in d["c"].items():     # a call's dispatches add up
+                cnt[i][k] = cnt[i].get(k, 0.0) + v
     groups = collections.OrderedDict()
     for i, (name, bound, fl, by, label) in enumerate(calls):
         g = groups.setdefault(label, {"name": name, "bound": bound, "flops": fl, "bytes": by,
