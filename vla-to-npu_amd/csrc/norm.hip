@@ -23,13 +23,19 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16* __restrict__ x
   const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   const bf16* xr = x + row * ldx;
-  bf16x8 v[MAXC];
+  // every load (row and gain) issued up front from a clamped address: a load
+  // under a branch would end its region with a full wait, one round trip each
+  bf16x8 v[MAXC], wv[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = min((lane + i * 64) * 8, cols - 8);
+    v[i] = ld8(xr + c);
+    wv[i] = ld8(w + c);
+  }
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {
-    const int c = (lane + i * 64) * 8;
-    if (c < cols) {
-      v[i] = ld8(xr + c);
+    if ((lane + i * 64) * 8 < cols) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const float f = bf2f(v[i][j]);
@@ -44,10 +50,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const bf16* __restrict__ x
   for (int i = 0; i < MAXC; ++i) {
     const int c = (lane + i * 64) * 8;
     if (c < cols) {
-      const bf16x8 wv = ld8(w + c);
       bf16x8 o;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = f2bf(__fmul_rn(__fmul_rn(bf2f(v[i][j]), r), bf2f(wv[j])));
+      for (int j = 0; j < 8; ++j) o[j] = f2bf(__fmul_rn(__fmul_rn(bf2f(v[i][j]), r), bf2f(wv[i][j])));
       st8(yr + c, o);
     }
   }
@@ -84,13 +89,21 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const bf16* __restrict__
   const int row = row0 + lane / LPR;
   const bool live = row < rows;
   const bf16* xr = x + (long)min(row, rows - 1) * ldx;
-  bf16x8 v[MAXC];
+  // every load (row, gamma, beta) issued up front from a clamped address: a
+  // load under a branch would end its region with a full wait
+  const bf16* bsrc = bta ? bta : gmm;
+  bf16x8 v[MAXC], gv[MAXC], bv[MAXC];
+#pragma unroll
+  for (int i = 0; i < MAXC; ++i) {
+    const int c = min((sub + i * LPR) * 8, cols - 8);
+    v[i] = ld8(xr + c);
+    gv[i] = ld8(gmm + c);
+    bv[i] = ld8(bsrc + c);
+  }
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < MAXC; ++i) {
-    const int c = (sub + i * LPR) * 8;
-    if (c < cols) {
-      v[i] = ld8(xr + c);
+    if ((sub + i * LPR) * 8 < cols) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) s += bf2f(v[i][j]);
     }
@@ -115,12 +128,10 @@ __global__ __launch_bounds__(256) void layernorm_kernel(const bf16* __restrict__
   for (int i = 0; i < MAXC; ++i) {
     const int c = (sub + i * LPR) * 8;
     if (c < cols) {
-      const bf16x8 gv = ld8(gmm + c);
-      bf16x8 bv = bta ? ld8(bta + c) : bf16x8{};
       bf16x8 o;
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        o[j] = f2bf((bf2f(v[i][j]) - mean) * rstd * bf2f(gv[j]) + bf2f(bv[j]));
+        o[j] = f2bf((bf2f(v[i][j]) - mean) * rstd * bf2f(gv[i][j]) + (bta ? bf2f(bv[i][j]) : 0.f));
       if constexpr (BLK)
         st8(y + (long)(c >> 5) * rows * 32 + (long)row * 32 + (c & 31), o);
       else
