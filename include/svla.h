@@ -286,12 +286,12 @@ int svla_action_out_euler(const void* a, int lda, const void* w, int ldw, float*
  * attention -> O + residual -> RMSNorm -> gate|up + SiLU*up -> down +
  * residual), the final RMSNorm + action_out and x <- x + dt * v -- in ONE
  * persistent launch for small batches (batch * chunk rows; chunk <= 64).
- * Rounding points of the reference torch modules: each RMSNorm output is
- * rounded once, bf16(x * (1/rms) * gain), before its projection (the
- * layer-by-layer GEMMs instead round bf16(x * gain) and scale by 1/rms in
- * their epilogue), projections round to bf16, RoPE runs in fp32 on the bf16
- * projection, the attention softmax is normalised before its probabilities
- * are rounded to bf16, residual adds round to bf16.  Replaces
+ * Rounding points of the reference torch modules (as on the layer-by-layer
+ * path): each RMSNorm output is rounded once, bf16((x * (1/rms)) * gain),
+ * before its projection; projections round to bf16; RoPE runs in fp32 on the
+ * bf16 projection and the scores take the fp32 result (bf16 hi + lo); the
+ * attention softmax is normalised before its probabilities are rounded to
+ * bf16; residual adds round to bf16.  Replaces
  * action_expert_self_forward / action_expert_cross_forward
  * (vla/action_expert_bf16.py:662-803) as driven by joint_transformer
  * (vla/vla.py:194-212) and postprocessing (vla/vla.py:218-222), plus the

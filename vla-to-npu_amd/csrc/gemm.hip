@@ -81,7 +81,7 @@ struct GemmArgs {
   // tokens straight into its slot of the [B, prefix_len, H] prefix buffer.
   int c_rpg;
   long c_gstride;
-  // fused RMSNorm of the A rows: a = bf16(x * rsqrt(mean(x^2) + eps) * w[k])
+  // fused RMSNorm of the A rows: a = bf16((x * r) * w[k]), r = 1 / sqrt(mean(x^2) + eps)
   const bf16* norm_w;
   float norm_eps;
   // skinny split-K (gridDim.z > 1): fp32 partial tiles [tile][split][BM * BN]
