@@ -530,6 +530,60 @@ def write_kernel_table(cfg, params, batch):
         f"{statistics.median(ts):.3f} ms per graph replay")
 
 
+def expert_phase_table(cfg, params, runs, out_path):
+    """Per-phase timing of the batch-1 fused expert (``plan.stamps``: the
+    team's first workgroup records the GPU's 100 MHz clock at every phase's
+    start and at its own arrival) over ``runs`` eager launches, each on the
+    chunk's own inputs; grouped by phase kind into ``out_path`` (markdown)."""
+    import collections
+    from smolvla.params import smolvla_inputs
+    from smolvla.pipeline import SmolVLAEngine
+    eng = SmolVLAEngine(cfg, params, batch=1)
+    inp = smolvla_inputs(cfg, 1, seed=1, device="cuda")
+    eng.run(*inp)                                   # prefix, cross K/V, a captured chunk
+    fx = eng.fx
+    kinds = fx.phase_kinds()
+    per = []
+    for _ in range(runs):
+        eng.x_t.copy_(eng.in_noise.view(-1, cfg.action_dim))
+        st = fx.phase_stamps().double() * 10.0 / 1e3     # 100 MHz ticks -> us
+        per.append(st)
+        if fx.status() != 0:
+            raise SystemExit("fused expert failed during the phase timing")
+    n = len(kinds)
+    if per[0].shape[0] != n:
+        raise SystemExit(f"phase count {per[0].shape[0]} != {n} named phases")
+    span = statistics.median(float(s[-1, 1] - s[0, 0]) for s in per)
+    groups = collections.OrderedDict()
+    for i, k in enumerate(kinds):
+        s2s = statistics.median(float((s[i + 1, 0] if i + 1 < n else s[i, 1]) - s[i, 0]) for s in per)
+        own = statistics.median(float(s[i, 1] - s[i, 0]) for s in per)
+        g = groups.setdefault(k, [0, 0.0, 0.0])
+        g[0] += 1
+        g[1] += s2s
+        g[2] += own
+    L = ["# Fused action expert, batch 1: time per phase kind\n",
+         "Command (repo root on the MI355X box): `python bench.py --expert-phases "
+         f"{runs}`\n",
+         f"One launch runs {n} dependent phases.  The team's first workgroup records the GPU's "
+         "100 MHz clock (`s_memrealtime`) when each phase starts (its wait for the previous "
+         "phase done) and after its own arrival (its units' stores acknowledged, its count "
+         "added): *start to start* is the phase's share of the launch's critical path, "
+         "*own unit* the first workgroup's work inside it (the rest is the hand-off: the last "
+         f"unit's arrival and the poll round trip).  Medians over {runs} eager launches on the "
+         "chunk's own inputs; stamps add two stores per phase to that workgroup.\n",
+         f"Launch span (first start to last arrival): {span / 1e3:.3f} ms, "
+         f"{span / n:.2f} us per phase.\n",
+         "| phase kind | phases | us start to start (mean) | us own unit (mean) | ms per launch | % |",
+         "|---|---:|---:|---:|---:|---:|"]
+    tot = sum(g[1] for g in groups.values())
+    for k, (c, s2s, own) in sorted(groups.items(), key=lambda kv: -kv[1][1]):
+        L.append(f"| {k} | {c} | {s2s / c:.2f} | {own / c:.2f} | {s2s / 1e3:.3f} | "
+                 f"{100 * s2s / tot:.1f} |")
+    pathlib.Path(out_path).write_text("\n".join(L) + "\n")
+    log(f"wrote {out_path}: {n} phases, span {span / 1e3:.3f} ms")
+
+
 def profile_chunks(cfg, params, batch, calls_out, eager_only):
     """Profiler entry point (``--profile-chunks``): the libsvla calls of one
     chunk at ``batch`` (with their work model and, unless ``eager_only``, the
@@ -618,6 +672,9 @@ def main():
     ap.add_argument("--out", default=None)
     ap.add_argument("--trace-cmd", default="")
     ap.add_argument("--pmc-cmd", action="append", default=[])
+    ap.add_argument("--expert-phases", type=int, metavar="RUNS",
+                    help="only write the batch-1 fused expert's per-phase timing (RUNS eager "
+                         "launches) to profiles/expert_phases_bs1.md")
     ap.add_argument("--kernel-table", type=int, metavar="BATCH",
                     help="only write the per-kernel census table of one chunk at this batch "
                          "to profiles/kernel_table_bs<BATCH>.md")
@@ -649,6 +706,10 @@ def main():
     params = smolvla_params(cfg, seed=0)
     if args.profile_chunks:
         profile_chunks(cfg, params, args.profile_chunks, args.calls_out, args.eager_only)
+        return
+    if args.expert_phases:
+        expert_phase_table(cfg, params, args.expert_phases,
+                           args.out or str(ROOT / "profiles" / "expert_phases_bs1.md"))
         return
     if args.kernel_table:
         write_kernel_table(cfg, params, args.kernel_table)

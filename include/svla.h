@@ -347,6 +347,12 @@ typedef struct svla_expert_plan {
                      about seconds); a caller may lower it, e.g. to exercise
                      the failure path: status 1 and NaN actions, every
                      workgroup still exits */
+  unsigned long long* stamps; /* optional (prepare: NULL), device memory of
+                     2 * n_phases counters: the first workgroup of the team
+                     records the GPU's constant 100 MHz clock
+                     (s_memrealtime) when phase p starts (its wait done) at
+                     stamps[2p] and after its own arrival at stamps[2p + 1]
+                     -- the per-phase timing of a run */
 } svla_expert_plan;
 
 /* Device workspace bytes svla_expert_prepare needs for d (phase table,

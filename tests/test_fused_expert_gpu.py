@@ -210,3 +210,27 @@ def test_expert_gives_up_loudly_with_a_tiny_spin_limit():
         fx.plan.spin_limit = limit
     again = eng.run(*dev).cpu()
     assert torch.equal(again, good)
+
+
+def test_phase_stamps(full1):
+    """plan.stamps: one start and one arrival clock stamp per phase from the
+    team's first workgroup, increasing through the launch (a phase starts
+    after the previous one's stamps), one per named phase; the run's actions
+    are bit-identical to a run without stamps."""
+    cfg, P, inputs, _ = full1
+    dev = [t.cuda() for t in inputs]
+    eng = _engine(cfg, P, 1, use_graph=False)
+    print("full config batch 1: fused expert with phase stamps", flush=True)
+    want = eng.run(*dev).cpu()
+    eng.x_t.copy_(eng.in_noise.view(-1, cfg.action_dim))
+    st = eng.fx.phase_stamps()
+    assert eng.fx.status() == 0
+    got = eng.x_t.view(1, cfg.chunk, cfg.action_dim).cpu()
+    assert torch.equal(got, want)
+    kinds = eng.fx.phase_kinds()
+    assert st.shape == (len(kinds), 2) == (eng.fx.plan.n_phases, 2)
+    flat = st.reshape(-1)
+    assert (flat > 0).all() and (flat[1:] >= flat[:-1]).all()
+    assert kinds[0] == "V^T transposes" and kinds[-1] == "action out + Euler"
+    span_ms = (st[-1, 1] - st[0, 0]).item() * 10 / 1e6
+    assert 0.5 < span_ms < 100, span_ms

@@ -152,6 +152,7 @@ struct XArgs {
   int team_xcd;      // < 0: every workgroup; else the workgroups on this XCD
   int team_size;     // participants expected when team_xcd >= 0
   int spin;          // polls before a wait gives up
+  unsigned long long* stamps;  // optional per-phase clock stamps (team rank 0)
 };
 
 // Loads through pointers read from the phase table: tell the compiler they
@@ -1123,6 +1124,7 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
         break;
       }
     }
+    if (g.stamps && rank == 0 && tidx() == 0) g.stamps[2 * p] = __builtin_amdgcn_s_memrealtime();
     if (P.kind == XK_GEMM) {
       for (int j = 0; j < mine; ++j) {
         const int u = rank + j * team;
@@ -1177,9 +1179,11 @@ __global__ __launch_bounds__(XT, 1) void expert_kernel(XArgs g) {
     // every store of this workgroup acknowledged, then one arrival
     __builtin_amdgcn_s_waitcnt(wc_vm(0));
     __syncthreads();
-    if (tid == 0)
+    if (tid == 0) {
       __hip_atomic_fetch_add(g.cnt + ((size_t)p * kSub + (rank & (kSub - 1))) * kCntStride,
                              (unsigned)mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (g.stamps && rank == 0) g.stamps[2 * p + 1] = __builtin_amdgcn_s_memrealtime();
+    }
   }
   if (failed) poison_actions(g);
 }
@@ -1465,6 +1469,7 @@ int svla_expert_prepare(const svla_expert_desc* d, void* ws, long ws_bytes, int 
   plan->team_xcd = team_xcd < 0 ? -1 : team_xcd;
   plan->team_size = team_xcd < 0 ? cus : cus / 8;
   plan->spin_limit = kSpin;
+  plan->stamps = nullptr;
   return SVLA_OK;
 }
 
@@ -1483,6 +1488,7 @@ int svla_expert_run(const svla_expert_plan* plan, svla_stream_t stream) {
   g.team_xcd = plan->team_xcd;
   g.team_size = plan->team_size;
   g.spin = plan->spin_limit;
+  g.stamps = plan->stamps;
   hipLaunchKernelGGL(expert_kernel, dim3(plan->grid), dim3(XT), 0, s, g);
   SVLA_CHECK_LAUNCH();
   return SVLA_OK;

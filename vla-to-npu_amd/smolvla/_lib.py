@@ -41,7 +41,7 @@ class ExpertPlan(ctypes.Structure):
     _fields_ = [("phases", _p), ("n_phases", ctypes.c_int), ("counters", _p),
                 ("counter_words", ctypes.c_long), ("status", _p), ("grid", ctypes.c_int),
                 ("team_xcd", ctypes.c_int), ("team_size", ctypes.c_int),
-                ("spin_limit", ctypes.c_int)]
+                ("spin_limit", ctypes.c_int), ("stamps", _p)]
 
 
 # name -> argtypes (all return int, except RESTYPES)

@@ -154,6 +154,38 @@ class FusedExpert:
         _lib.call("svla_expert_status", ctypes.byref(self.plan), ctypes.byref(st))
         return st.value
 
+    def phase_stamps(self):
+        """One eager run with per-phase clock stamps (``plan.stamps``):
+        ``[n_phases, 2]`` int64 ticks of the GPU's 100 MHz clock, the phase's
+        start (its wait done) and its arrival, on the team's first workgroup.
+        Synchronous.  A graph captured before keeps launching without stamps."""
+        n = self.plan.n_phases
+        buf = torch.zeros(2 * n, dtype=torch.int64, device=self.workspace.device)
+        self.plan.stamps = buf.data_ptr()
+        try:
+            self.run()
+            torch.cuda.synchronize(self.workspace.device)
+        finally:
+            self.plan.stamps = None
+        return buf.view(n, 2).cpu()
+
+    def phase_kinds(self):
+        """Name of every phase of the launch, in order: the cross layers'
+        V^T transposes (one phase), then per Euler step action-in, time-in,
+        time-out, per layer norm + QKV / Q + RoPE, attention, O + residual,
+        norm + gate|up + SiLU, down + residual, and action-out + Euler."""
+        names = ["V^T transposes"] if any(l.cross for l in self.layers) else []
+        per_layer = ("norm + {} + RoPE", "{} attention", "O + residual",
+                     "norm + gate|up + SiLU", "down + residual")
+        for _ in range(self.desc.num_steps):
+            names += ["action in", "time in + SiLU", "time out"]
+            for lay in self.layers:
+                kind = "cross" if lay.cross else "self"
+                qkv = "Q" if lay.cross else "QKV"
+                names += [per_layer[0].format(qkv), per_layer[1].format(kind)] + list(per_layer[2:])
+            names.append("action out + Euler")
+        return names
+
     def trace(self, step, layer):
         """The activation entering expert layer ``layer`` at Euler step
         ``step`` of the last run (``layer == n_layers``: the last layer's
