@@ -726,23 +726,21 @@ extern "C" int svla_attention_lo_bf16(const void* q, const void* q_lo, int ldq, 
   const bool full = mask_kind == SVLA_MASK_NONE && sk % BKEY == 0 && lo == 0;
   hipStream_t s = (hipStream_t)stream;
   if (lo > 0 && sk <= SHORT_KEYS) {
-    // RoPE'd layers: the single-pass exact form.  Up to 64 queries (the
-    // expert): one workgroup per (sample, KV head) holding all its query
-    // heads (hpw = hq / hkv, 4 query tiles each) when that fits 16 waves;
-    // longer ranges (the prefix): one head, up to 16 query tiles (256 rows),
-    // fewer (down to 4) while the grid has under 128 workgroups, each then
-    // staging the head's K / V for its own query tiles.  Measured on MI355X,
-    // prefix 241 x 241, 15 / 5 heads, bit-identical: batch 1 12.7 -> 7.2 us
-    // (4 tiles: 60 workgroups), batch 2 12.9 -> 7.5 us; batch 32 keeps 16
-    // (35.7 us against 43.9 with 8).
+    // RoPE'd layers: the single-pass exact form, one query head per
+    // workgroup (the kernel can also give a KV group's hpw query heads one
+    // workgroup that stages their K / V once; one head each measured as fast
+    // or faster on MI355X, bit-identical: the expert's 50 x 241 cross
+    // attention at batch 32 10.8 / 10.9 us, batch 1 9.4 -> 6.5 us; 50 x 50
+    // self attention at batch 32 6.2 -> 5.3 us, batch 1 5.5 -> 4.0 us).  Up
+    // to 16 query tiles (256 rows) per workgroup, fewer (down to 4) while
+    // the grid has under 128 workgroups, each workgroup then staging the
+    // head's K / V for its own query tiles (prefix 241 x 241, 15 / 5 heads:
+    // batch 1 12.7 -> 7.2 us with 4 tiles, 60 workgroups; batch 2 12.9 ->
+    // 7.5 us; batch 32 keeps 16: 35.7 us against 43.9 with 8).
     const int tiles = (sq + 15) / 16;
-    int hpw = 1, qtiles = min(tiles, 16);
-    if (tiles <= 4 && (hq / hkv) * tiles <= 16) {
-      hpw = hq / hkv;
-      qtiles = tiles;
-    } else {
-      while (qtiles > 4 && (long)((tiles + qtiles - 1) / qtiles) * hq * batch < 128) qtiles /= 2;
-    }
+    const int hpw = 1;
+    int qtiles = min(tiles, 16);
+    while (qtiles > 4 && (long)((tiles + qtiles - 1) / qtiles) * hq * batch < 128) qtiles /= 2;
     dim3 grid((tiles + qtiles - 1) / qtiles, hq / hpw, batch);
     const dim3 block(64 * hpw * qtiles);
     if (sk <= BKEY) {
