@@ -93,18 +93,24 @@ def time_chunks(eng, n):
     return out
 
 
-def _up_proj_launcher(cfg, M, x, w_packed, bias, wide):
+def _up_proj_launcher(cfg, M, x, w_packed, bias):
     """The ViT MLP up-projection exactly as the engine launches it at this
-    row count: on the 256x256 kernel with slab-blocked activations (the
-    LayerNorm writes them so), weights and output when ``wide``
-    (``layers.vit_wide_ok``), else through ``ops.linear``."""
-    from smolvla import ops
+    row count (``layers.vit_blocked_plan``): on the 256x256 kernel with
+    slab-blocked activations (the LayerNorm writes them so) and weights, and
+    a slab-blocked output when the down-projection reads it so; else through
+    ``ops.linear``."""
+    from smolvla import layers, ops
     v = cfg.vit
-    if wide:
+    plan = layers.vit_blocked_plan(v.hidden, v.inter, M)
+    if plan["up"]:
         xb = ops.slab_block(x)
         wb = ops.slab_block(w_packed)
-        out = torch.empty(v.inter // 32, M, 32, device="cuda", dtype=torch.bfloat16)
-        lay = ops.LAYOUT_A_BLOCKED | ops.LAYOUT_W_BLOCKED | ops.LAYOUT_C_BLOCKED
+        lay = ops.LAYOUT_A_BLOCKED | ops.LAYOUT_W_BLOCKED
+        if plan["down"]:
+            lay |= ops.LAYOUT_C_BLOCKED
+            out = torch.empty(v.inter // 32, M, 32, device="cuda", dtype=torch.bfloat16)
+        else:
+            out = torch.empty(M, v.inter, device="cuda", dtype=torch.bfloat16)
         return lambda: ops.linear_wide(xb, wb, M, v.inter, v.hidden, bias=bias,
                                        act="gelu_" + v.gelu, out=out, layout=lay)
     out = torch.empty(M, v.inter, device="cuda", dtype=torch.bfloat16)
@@ -160,8 +166,7 @@ def traffic_probe(cfg, batch):
     x = torch.randn(M, v.hidden, device="cuda", generator=g).to(torch.bfloat16)
     w = (torch.randn(v.inter, v.hidden, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
     b = (torch.randn(v.inter, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
-    from smolvla import layers
-    run = _up_proj_launcher(cfg, M, x, w, b, layers.vit_wide_ok(v, M))
+    run = _up_proj_launcher(cfg, M, x, w, b)
     torch.cuda.synchronize()
     for _ in range(3):
         run()

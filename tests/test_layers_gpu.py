@@ -197,29 +197,39 @@ def test_joint_transformer_two_layers():
     check(got, want[0])
 
 
+VIT_PLANS = {"all": {"qkv", "o", "up", "down"},     # batch 4 and up
+             "qkv+up": {"qkv", "up"},                 # batches 2-3: row-major MLP activation
+             "up": {"up"}}                            # batch 1
+
+
+@pytest.mark.parametrize("plan", list(VIT_PLANS))
 @pytest.mark.parametrize("biases", [True, False])
-def test_vit_layer_wide_blocked(biases):
-    """The ViT block on the 256x256 GEMM with slab-blocked weights and a
-    slab-blocked MLP activation (the batch-32 engine's path) against the
-    oracle, and bit-identical to the row-major path forced onto the same
-    kernel."""
-    from smolvla import _lib, layers
+def test_vit_layer_blocked_plans(biases, plan):
+    """The ViT block with each mix of projections that the engine runs on the
+    256x256 GEMM with slab-blocked operands, against the oracle, and
+    bit-identical to the all-row-major path with every GEMM forced onto the
+    same kernel."""
+    from smolvla import _lib, layers, ops
     cfg = VitConfig()
     p = vit_layer_params(_Gen(124, norm_init="random"), cfg, biases=biases)
     x = x_in(125, 2, 1024, 768)
     want = ref.vit_block(x, p, cfg)
-    P = layers.prep_vit(p, "cuda", wide=True)
-    xg = x.reshape(2048, 768).cuda()
-    layers.vit_layer(xg, P, cfg, 2, 1024)
-    check(xg.view(2, 1024, 768), want)
+    P = layers.prep_vit(p, "cuda")
+    assert not any(P["blk"].values())
+    Pb = dict(P, blk={k: k in VIT_PLANS[plan] for k in layers.VIT_PROJ})
+    for k in VIT_PLANS[plan]:
+        w = layers.VIT_PROJ[k]
+        Pb[w + "_blk"] = ops.slab_block(P[w])
     lib = _lib.load()
     lib.svla_gemm_set_tile(8)
     try:
-        Pr = dict(P, wide=False)
+        xg = x.reshape(2048, 768).cuda()
+        layers.vit_layer(xg, Pb, cfg, 2, 1024)
         xr = x.reshape(2048, 768).cuda()
-        layers.vit_layer(xr, Pr, cfg, 2, 1024)
+        layers.vit_layer(xr, P, cfg, 2, 1024)
     finally:
         lib.svla_gemm_set_tile(-1)
+    check(xg.view(2, 1024, 768), want)
     assert torch.equal(xr, xg)
 
 

@@ -109,10 +109,10 @@ def prep_cross(p, device):
     )
 
 
-def prep_vit(p, device, wide=False):
-    """Packed ViT block weights.  ``wide``: also slab-blocked copies for the
-    256x256 GEMM (``ops.linear_wide``), used when every ViT projection at the
-    engine's row count runs on that kernel."""
+def prep_vit(p, device, rows=None):
+    """Packed ViT block weights.  ``rows`` (the engine's row count, images x
+    tokens): also slab-blocked copies of the weights that
+    :func:`vit_blocked_plan` puts on the 256x256 GEMM at that row count."""
     H = p["Wq"].shape[0]
     bqkv = None
     if p.get("bq") is not None:
@@ -127,24 +127,40 @@ def prep_vit(p, device, wide=False):
         wd=ops.pack_weight(_dev(p["W_down"], device)), bd=opt("b_down"),
         g1=_dev(p["W_norm_1"], device), b1=opt("b_norm_1"),
         g2=_dev(p["W_norm_2"], device), b2=opt("b_norm_2"),
-        wide=wide,
     )
-    if wide:
-        for k in ("wqkv", "wo", "wup", "wd"):
-            P[k + "_blk"] = ops.slab_block(P[k])
+    I = P["wup"].shape[0]
+    P["blk"] = vit_blocked_plan(H, I, rows) if rows else dict.fromkeys(VIT_PROJ, False)
+    for k, w in VIT_PROJ.items():
+        if P["blk"][k]:
+            P[w + "_blk"] = ops.slab_block(P[w])
     return P
 
 
-def vit_wide_ok(cfg: VitConfig, rows: int) -> bool:
-    """True when the 256x256 GEMM takes every ViT projection at ``rows`` rows
-    (the automatic tile choice), so the slab-blocked layouts can be used."""
-    from . import _lib
-    lib = _lib.load()
-    H, I = cfg.hidden, cfg.inter
-    shapes = ((3 * H, H), (H, H), (I, H), (H, I))
-    return rows % 256 == 0 and all(n % 256 == 0 and k % 128 == 0 and
-                                   lib.svla_gemm_tile_choice(rows, n, k, 0) == 8
-                                   for n, k in shapes)
+VIT_PROJ = {"qkv": "wqkv", "o": "wo", "up": "wup", "down": "wd"}
+
+# The 256x256 GEMM on slab-blocked operands beats the automatic tile choice on
+# row-major operands once a projection has at least this many 256x256 output
+# tiles (MI355X, the SigLIP shapes at 1-10 images of 3 cameras: QKV wins from
+# 216 tiles and loses at 108, O and down win from 144 and lose at 108, the
+# up-projection wins from 144).
+WIDE_MIN_TILES = 144
+
+
+def vit_blocked_plan(hidden: int, inter: int, rows: int) -> dict:
+    """Which ViT projections run on the 256x256 GEMM with slab-blocked
+    weights at ``rows`` rows: those whose shape the kernel takes and that
+    have at least ``WIDE_MIN_TILES`` output tiles.  QKV and the
+    up-projection then read a slab-blocked LayerNorm output; the
+    down-projection reads the up-projection's output slab-blocked, so it goes
+    blocked only together with the up-projection; O reads the attention
+    output row-major.  Every choice computes the same bits."""
+    shapes = {"qkv": (3 * hidden, hidden), "o": (hidden, hidden),
+              "up": (inter, hidden), "down": (hidden, inter)}
+    plan = {name: (rows % 256 == 0 and n % 256 == 0 and k % 128 == 0 and k >= 256 and
+                   (rows // 256) * (n // 256) >= WIDE_MIN_TILES)
+            for name, (n, k) in shapes.items()}
+    plan["down"] = plan["down"] and plan["up"]
+    return plan
 
 
 @dataclass
@@ -274,44 +290,48 @@ def cross_layer(x, ck, cv, P, cfg: DecoderConfig, B, L, Lc, rope: Rope,
 
 def vit_layer(x, P, cfg: VitConfig, n_img, T, bufs: Optional[Buffers] = None):
     """SigLIP-style block on ``x [n_img*T, H]`` in place
-    (vla/vision_block_bf16.py:308-420)."""
-    bufs = bufs or Buffers(x.device)
-    M = n_img * T
-    H = cfg.hidden
-    if P.get("wide"):
-        return _vit_layer_wide(x, P, cfg, n_img, T, bufs)
-    h = ops.layernorm(x, P["g1"], P["b1"], cfg.ln_eps, out=bufs.get("vh", M, H))
-    qkv = ops.linear(h, P["wqkv"], bias=P["bqkv"], out=bufs.get("vqkv", M, 3 * H))
-    q3 = qkv.view(n_img, T, 3 * H)
-    attn = bufs.get("vattn", M, H)
-    ops.attention(q3[:, :, :H], q3[:, :, H:2 * H], q3[:, :, 2 * H:], attn.view(n_img, T, H),
-                  cfg.n_heads, cfg.n_heads, "none", 0, scale=1.0 / math.sqrt(cfg.head_dim))
-    ops.linear(attn, P["wo"], bias=P["bo"], res=x, out=x)
-    h = ops.layernorm(x, P["g2"], P["b2"], cfg.ln_eps, out=bufs.get("vh", M, H))
-    act = ops.linear(h, P["wup"], bias=P["bup"], act="gelu_" + cfg.gelu,
-                     out=bufs.get("vmlp", M, cfg.inter))
-    ops.linear(act, P["wd"], bias=P["bd"], res=x, out=x)
-
-
-def _vit_layer_wide(x, P, cfg: VitConfig, n_img, T, bufs: Buffers):
-    """The same block on the 256x256 GEMM with slab-blocked weights; the
-    LayerNorm outputs and the MLP hidden activations are written slab-blocked
-    too, so every projection's K loop streams both operands as contiguous
-    kilobytes (the residual stream stays row-major).  Same arithmetic as
-    :func:`vit_layer` on that kernel, bit for bit."""
+    (vla/vision_block_bf16.py:308-420).  Each projection that ``P["blk"]``
+    marks runs on the 256x256 GEMM with slab-blocked weights, and the
+    LayerNorm output (or MLP activation) it reads is written slab-blocked, so
+    its K loop streams both operands as contiguous kilobytes; the others run
+    on the automatic tile choice.  The residual stream stays row-major."""
     from .ops import LAYOUT_A_BLOCKED as AB, LAYOUT_W_BLOCKED as WB, LAYOUT_C_BLOCKED as CB
+    bufs = bufs or Buffers(x.device)
     M, H, I = n_img * T, cfg.hidden, cfg.inter
-    hb = bufs.get("vh", M, H).view(H // 32, M, 32)
-    ops.layernorm(x, P["g1"], P["b1"], cfg.ln_eps, out=hb, blocked=True)
-    qkv = ops.linear_wide(hb, P["wqkv_blk"], M, 3 * H, H, bias=P["bqkv"],
-                          out=bufs.get("vqkv", M, 3 * H), layout=AB | WB)
+    blk = P["blk"]
+
+    def norm(g, b, blocked):
+        out = bufs.get("vh", M, H)
+        if blocked:
+            return ops.layernorm(x, g, b, cfg.ln_eps, out=out.view(H // 32, M, 32), blocked=True)
+        return ops.layernorm(x, g, b, cfg.ln_eps, out=out)
+
+    h = norm(P["g1"], P["b1"], blk["qkv"])
+    qkv = bufs.get("vqkv", M, 3 * H)
+    if blk["qkv"]:
+        ops.linear_wide(h, P["wqkv_blk"], M, 3 * H, H, bias=P["bqkv"], out=qkv, layout=AB | WB)
+    else:
+        ops.linear(h, P["wqkv"], bias=P["bqkv"], out=qkv)
     q3 = qkv.view(n_img, T, 3 * H)
     attn = bufs.get("vattn", M, H)
     ops.attention(q3[:, :, :H], q3[:, :, H:2 * H], q3[:, :, 2 * H:], attn.view(n_img, T, H),
                   cfg.n_heads, cfg.n_heads, "none", 0, scale=1.0 / math.sqrt(cfg.head_dim))
-    ops.linear_wide(attn, P["wo_blk"], M, H, H, bias=P["bo"], res=x, out=x, layout=WB)
-    ops.layernorm(x, P["g2"], P["b2"], cfg.ln_eps, out=hb, blocked=True)
-    act = bufs.get("vmlp", M, I).view(I // 32, M, 32)
-    ops.linear_wide(hb, P["wup_blk"], M, I, H, bias=P["bup"], act="gelu_" + cfg.gelu, out=act,
-                    layout=AB | WB | CB)
-    ops.linear_wide(act, P["wd_blk"], M, H, I, bias=P["bd"], res=x, out=x, layout=AB | WB)
+    if blk["o"]:
+        ops.linear_wide(attn, P["wo_blk"], M, H, H, bias=P["bo"], res=x, out=x, layout=WB)
+    else:
+        ops.linear(attn, P["wo"], bias=P["bo"], res=x, out=x)
+    h = norm(P["g2"], P["b2"], blk["up"])
+    gelu = "gelu_" + cfg.gelu
+    act = bufs.get("vmlp", M, I)
+    if blk["down"]:                       # up is blocked too: hand the activation over blocked
+        act = act.view(I // 32, M, 32)
+        ops.linear_wide(h, P["wup_blk"], M, I, H, bias=P["bup"], act=gelu, out=act,
+                        layout=AB | WB | CB)
+        ops.linear_wide(act, P["wd_blk"], M, H, I, bias=P["bd"], res=x, out=x, layout=AB | WB)
+        return
+    if blk["up"]:
+        ops.linear_wide(h, P["wup_blk"], M, I, H, bias=P["bup"], act=gelu, out=act,
+                        layout=AB | WB)
+    else:
+        ops.linear(h, P["wup"], bias=P["bup"], act=gelu, out=act)
+    ops.linear(act, P["wd"], bias=P["bd"], res=x, out=x)

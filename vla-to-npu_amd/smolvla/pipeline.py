@@ -67,8 +67,8 @@ class SmolVLAEngine:
         self.patch_w = pd(P["patch"]["kernel"]).reshape(v.hidden, -1)
         self.patch_b = pd(P["patch"]["bias"])
         self.pos_emb = pd(P["patch"]["pos_emb"])
-        wide = layers.vit_wide_ok(v, self.B * cfg.n_cameras * v.tokens)
-        self.vit = [layers.prep_vit(lp, dev, wide=wide) for lp in P["vit"]]
+        vit_rows = self.B * cfg.n_cameras * v.tokens
+        self.vit = [layers.prep_vit(lp, dev, rows=vit_rows) for lp in P["vit"]]
         self.conn_w = ops.pack_weight(pd(P["connector"]["W"]))
         self.embed_table = pd(P["embed"])
         self.state_w = ops.pack_weight(pd(P["state"]["W"]))
