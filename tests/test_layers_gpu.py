@@ -215,8 +215,8 @@ def test_vit_layer_blocked_plans(biases, plan):
     x = x_in(125, 2, 1024, 768)
     want = ref.vit_block(x, p, cfg)
     P = layers.prep_vit(p, "cuda")
-    assert not any(P["blk"].values())
-    Pb = dict(P, blk={k: k in VIT_PLANS[plan] for k in layers.VIT_PROJ})
+    assert not any(k.endswith("_blk") for k in P)
+    Pb = dict(P)
     for k in VIT_PLANS[plan]:
         w = layers.VIT_PROJ[k]
         Pb[w + "_blk"] = ops.slab_block(P[w])
@@ -224,13 +224,21 @@ def test_vit_layer_blocked_plans(biases, plan):
     lib.svla_gemm_set_tile(8)
     try:
         xg = x.reshape(2048, 768).cuda()
-        layers.vit_layer(xg, Pb, cfg, 2, 1024)
+        layers.vit_layer(xg, Pb, cfg, 2, 1024, plan=dict.fromkeys(layers.VIT_PROJ, True))
         xr = x.reshape(2048, 768).cuda()
-        layers.vit_layer(xr, P, cfg, 2, 1024)
+        layers.vit_layer(xr, Pb, cfg, 2, 1024, plan=dict.fromkeys(layers.VIT_PROJ, False))
     finally:
         lib.svla_gemm_set_tile(-1)
     check(xg.view(2, 1024, 768), want)
     assert torch.equal(xr, xg)
+    if plan == "all":
+        # weights prepared for 12 images, called on 2: the plan at the call's
+        # 2048 rows (no projection has 144 tiles) takes the row-major path
+        P12 = layers.prep_vit(p, "cuda", rows=12 * 1024)
+        assert all(w + "_blk" in P12 for w in layers.VIT_PROJ.values())
+        x2 = x.reshape(2048, 768).cuda()
+        layers.vit_layer(x2, P12, cfg, 2, 1024)
+        check(x2.view(2, 1024, 768), want)
 
 
 @pytest.mark.parametrize("rows", [241, 482])

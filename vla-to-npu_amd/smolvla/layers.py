@@ -128,11 +128,11 @@ def prep_vit(p, device, rows=None):
         g1=_dev(p["W_norm_1"], device), b1=opt("b_norm_1"),
         g2=_dev(p["W_norm_2"], device), b2=opt("b_norm_2"),
     )
-    I = P["wup"].shape[0]
-    P["blk"] = vit_blocked_plan(H, I, rows) if rows else dict.fromkeys(VIT_PROJ, False)
-    for k, w in VIT_PROJ.items():
-        if P["blk"][k]:
-            P[w + "_blk"] = ops.slab_block(P[w])
+    if rows:
+        plan = vit_blocked_plan(H, P["wup"].shape[0], rows)
+        for k, w in VIT_PROJ.items():
+            if plan[k]:
+                P[w + "_blk"] = ops.slab_block(P[w])
     return P
 
 
@@ -288,17 +288,20 @@ def cross_layer(x, ck, cv, P, cfg: DecoderConfig, B, L, Lc, rope: Rope,
     _mlp(x, P, cfg, M, eps, bufs)
 
 
-def vit_layer(x, P, cfg: VitConfig, n_img, T, bufs: Optional[Buffers] = None):
+def vit_layer(x, P, cfg: VitConfig, n_img, T, bufs: Optional[Buffers] = None, plan=None):
     """SigLIP-style block on ``x [n_img*T, H]`` in place
-    (vla/vision_block_bf16.py:308-420).  Each projection that ``P["blk"]``
-    marks runs on the 256x256 GEMM with slab-blocked weights, and the
+    (vla/vision_block_bf16.py:308-420).  Each projection that ``plan``
+    (default: :func:`vit_blocked_plan` at these rows) marks and whose
+    slab-blocked weight ``P`` holds runs on the 256x256 GEMM, and the
     LayerNorm output (or MLP activation) it reads is written slab-blocked, so
     its K loop streams both operands as contiguous kilobytes; the others run
     on the automatic tile choice.  The residual stream stays row-major."""
     from .ops import LAYOUT_A_BLOCKED as AB, LAYOUT_W_BLOCKED as WB, LAYOUT_C_BLOCKED as CB
     bufs = bufs or Buffers(x.device)
     M, H, I = n_img * T, cfg.hidden, cfg.inter
-    blk = P["blk"]
+    plan = plan or vit_blocked_plan(H, I, M)
+    blk = {k: bool(plan[k]) and w + "_blk" in P for k, w in VIT_PROJ.items()}
+    blk["down"] = blk["down"] and blk["up"]
 
     def norm(g, b, blocked):
         out = bufs.get("vh", M, H)
