@@ -157,6 +157,38 @@ def test_batch32_engine_matches_oracle_and_batch1():
     assert worst <= ACTION_ATOL
 
 
+@pytest.mark.parametrize("B", [2, 4])
+def test_mid_batch_engines_match_batch1(B):
+    """Batch 2 (QKV and the up-projection on the 256x256 kernel with
+    slab-blocked operands, the MLP activation handed to the down-projection
+    row-major) and batch 4 (every ViT projection on it), layer-by-layer
+    expert: each sample's vision output and actions against the batch-1
+    engine (fused expert, its own tile choices)."""
+    from smolvla import layers
+    from smolvla.pipeline import SmolVLAEngine
+    cfg = SmolVLAConfig()
+    v = cfg.vit
+    plan = layers.vit_blocked_plan(v.hidden, v.inter, B * cfg.n_cameras * v.tokens)
+    assert {k for k, on in plan.items() if on} == ({"qkv", "up"} if B == 2 else set(plan))
+    P = smolvla_params(cfg, seed=0, norm_init="random")
+    inputs = smolvla_inputs(cfg, batch=B, seed=9)
+    eng = SmolVLAEngine(cfg, P, batch=B, use_graph=True)
+    got = eng.run(*[t.cuda() for t in inputs]).cpu()
+    vis = eng.vit_x.view(B, -1, v.hidden).cpu()
+    del eng
+    torch.cuda.empty_cache()
+    one = SmolVLAEngine(cfg, P, batch=1, use_graph=True)
+    worst_act, worst_vis = 0.0, 0.0
+    for b in range(B):
+        r = one.run(*[t[b:b + 1].cuda() for t in inputs]).cpu()
+        worst_act = max(worst_act, (r - got[b:b + 1]).abs().max().item())
+        worst_vis = max(worst_vis, rel_err(vis[b], one.vit_x.view(-1, v.hidden).cpu()))
+    print(f"batch {B} vs batch-1 engine: vision max-rel {worst_vis:.3e}, actions max abs "
+          f"{worst_act:.3e}")
+    assert worst_vis <= STAGE_MAX_REL
+    assert worst_act <= ACTION_ATOL
+
+
 @pytest.mark.parametrize("fused", [True, False])
 def test_batch1_replays_bit_stable(full, fused):
     """The batch-1 engine (the latency path: skinny and 64x64 LDS-DMA GEMMs,
