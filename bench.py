@@ -535,6 +535,45 @@ def write_kernel_table(cfg, params, batch):
         f"{statistics.median(ts):.3f} ms per graph replay")
 
 
+def batch_sweep(cfg, params, batches, out_path):
+    """Chunk time and throughput at each batch size in ``batches`` (one engine
+    each, graph replays, median of 10 after 3 warm-ups), with the engine's
+    expert path and the ViT projections on the slab-blocked 256x256 GEMM, into
+    ``out_path`` (markdown)."""
+    from smolvla import layers
+    from smolvla.params import smolvla_inputs
+    from smolvla.pipeline import SmolVLAEngine
+    v = cfg.vit
+    L = ["# Chunk time against batch size (bench.py --batch-sweep)\n",
+         "Command (repo root on the MI355X box): `python bench.py --batch-sweep "
+         + " ".join(map(str, batches)) + "`\n",
+         "One engine per batch size (seeded random-init bf16 weights, synthetic inputs resident "
+         "in HBM); each chunk is one HIP-graph replay, median of 10 after 3 warm-ups, timed with "
+         "HIP events on the engine's stream.  *ViT on 256x256*: the projections that "
+         "`layers.vit_blocked_plan` puts on the slab-blocked 256x256 GEMM at that row count.  "
+         "Boxes differ by up to +-15% in clock.\n",
+         "| batch | expert | ViT on 256x256 | ms per chunk | chunks/s | TFLOP/s end to end |",
+         "|---:|---|---|---:|---:|---:|"]
+    for b in batches:
+        eng = SmolVLAEngine(cfg, params, batch=b)
+        eng.load_inputs(*smolvla_inputs(cfg, b, seed=1, device="cuda"))
+        eng.capture()
+        for _ in range(3):
+            eng.step()
+        ms = statistics.median(time_chunks(eng, 10))
+        eng.check()
+        plan = layers.vit_blocked_plan(v.hidden, v.inter, b * cfg.n_cameras * v.tokens)
+        on = ", ".join(k for k, x in plan.items() if x) or "none"
+        kind = "fused (one launch)" if eng.fx is not None else "layer by layer"
+        L.append(f"| {b} | {kind} | {on} | {ms:.3f} | {b / ms * 1e3:.1f} | "
+                 f"{chunk_flops(cfg, b) / (ms * 1e-3) / 1e12:.1f} |")
+        log(f"batch {b}: {ms:.3f} ms per chunk, {b / ms * 1e3:.1f} chunks/s")
+        del eng
+        torch.cuda.empty_cache()
+    pathlib.Path(out_path).write_text("\n".join(L) + "\n")
+    log(f"wrote {out_path}")
+
+
 def expert_phase_table(cfg, params, runs, out_path):
     """Per-phase timing of the batch-1 fused expert (``plan.stamps``: the
     team's first workgroup records the GPU's 100 MHz clock at every phase's
@@ -680,6 +719,8 @@ def main():
     ap.add_argument("--expert-phases", type=int, metavar="RUNS",
                     help="only write the batch-1 fused expert's per-phase timing (RUNS eager "
                          "launches) to profiles/expert_phases_bs1.md")
+    ap.add_argument("--batch-sweep", type=int, nargs="+", metavar="BATCH",
+                    help="chunk time and chunks/s at each batch size -> profiles/batch_sweep.md")
     ap.add_argument("--kernel-table", type=int, metavar="BATCH",
                     help="only write the per-kernel census table of one chunk at this batch "
                          "to profiles/kernel_table_bs<BATCH>.md")
@@ -718,6 +759,10 @@ def main():
         return
     if args.kernel_table:
         write_kernel_table(cfg, params, args.kernel_table)
+        return
+    if args.batch_sweep:
+        batch_sweep(cfg, params, args.batch_sweep,
+                    args.out or str(ROOT / "profiles" / "batch_sweep.md"))
         return
     B = args.batch
     log(f"preparing engine at batch {B}")
