@@ -189,6 +189,26 @@ def test_mid_batch_engines_match_batch1(B):
     assert worst_act <= ACTION_ATOL
 
 
+def test_batch32_replays_bit_stable():
+    """The batch-32 engine bench.py times (persistent slab-blocked ViT GEMMs,
+    the skinny split-K workspace, the layer-by-layer expert) gives the same
+    bits on every graph replay, with other work on the device between the
+    replays, and in eager mode."""
+    from smolvla.pipeline import SmolVLAEngine
+    cfg = SmolVLAConfig()
+    P = smolvla_params(cfg, seed=0, norm_init="random")
+    B = 32
+    dev = [t.cuda() for t in smolvla_inputs(cfg, batch=B, seed=7)]
+    eng = SmolVLAEngine(cfg, P, batch=B)
+    first = eng.run(*dev).clone()
+    assert torch.isfinite(first).all()
+    for i in range(3):
+        torch.randn(1 << 22, device="cuda").sum().item()
+        assert torch.equal(eng.run(*dev), first), f"replay {i} differs"
+    eng.use_graph = False
+    assert torch.equal(eng.run(*dev), first), "eager run differs"
+
+
 @pytest.mark.parametrize("fused", [True, False])
 def test_batch1_replays_bit_stable(full, fused):
     """The batch-1 engine (the latency path: skinny and 64x64 LDS-DMA GEMMs,
